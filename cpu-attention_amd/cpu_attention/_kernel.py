@@ -1,0 +1,445 @@
+"""Loads the gfx950 kernel library and exposes the reference's native entries.
+
+The reference loads a Mojo CPython extension per CPU tier (cpu_attention/_kernel.py:52-84
+of ducviet00/cpu-attention) whose entries ``decode``, ``store`` and ``flash``
+(_mojo/src/_C.mojo:87-316) read torch tensors in place, validate them, and return
+``None`` for anything they do not take.  This build keeps that module surface --
+``module().decode/.store/.flash`` with the same positional arguments and the same
+``None`` / ``int`` return conventions -- but the entries are thin Python shims:
+they read tensor metadata through torch's public API, apply the same acceptance
+rules, allocate outputs with ``torch.empty`` on the tensors' GPU, and call the
+C ABI of ``libcpu_attention_hip.so`` (include/cpu_attention_hip.h) through
+ctypes on torch's current HIP stream.  The kernels run asynchronously.
+
+Data-dependent rules (a slot past the cache's end, a length beyond the page
+table's capacity) need the index values.  By default they are checked on the
+host exactly as the reference does, which reads the index tensors (a device
+synchronisation when they live on the GPU).  ``set_host_checks(False)`` (or
+``CPU_ATTENTION_HOST_CHECKS=0``) skips that read: the kernels never access memory
+out of bounds either way (such tokens are not stored, such positions not read),
+but no ValueError is raised.
+
+Environment: ``CPU_ATTENTION_LIB`` names another build of the library.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+DTYPES = {torch.float32: 0, torch.bfloat16: 1}
+HEAD_DIMS = (32, 64, 128)
+_DIR = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = "libcpu_attention_hip.so"
+ABI_VERSION = 1
+_ESIZE = {torch.float32: 4, torch.bfloat16: 2}
+_PLAIN = (torch.Tensor, torch.nn.Parameter)
+
+CA_OK, CA_DECLINED = 0, 1
+
+
+class StoreArgs(ctypes.Structure):
+    """``ca_store_args`` (include/cpu_attention_hip.h)."""
+    _fields_ = [
+        ("key", ctypes.c_void_p), ("value", ctypes.c_void_p), ("token_stride", ctypes.c_int64),
+        ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+        ("slot_mapping", ctypes.c_void_p), ("num_tokens", ctypes.c_int64),
+        ("num_heads", ctypes.c_int64), ("head_dim", ctypes.c_int64),
+        ("page_size", ctypes.c_int64), ("num_blocks", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+    ]
+
+
+class DecodeArgs(ctypes.Structure):
+    """``ca_decode_args`` (include/cpu_attention_hip.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("q_stride", ctypes.c_int64),
+        ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+        ("k_new", ctypes.c_void_p), ("v_new", ctypes.c_void_p), ("kv_stride", ctypes.c_int64),
+        ("slots", ctypes.c_void_p), ("lens", ctypes.c_void_p), ("page_table", ctypes.c_void_p),
+        ("page_table_width", ctypes.c_int64), ("out", ctypes.c_void_p),
+        ("num_seqs", ctypes.c_int64), ("num_heads", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64), ("page_size", ctypes.c_int64),
+        ("num_blocks", ctypes.c_int64), ("scale", ctypes.c_float), ("dtype", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
+class FlashArgs(ctypes.Structure):
+    """``ca_flash_args`` (include/cpu_attention_hip.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("out", ctypes.c_void_p), ("batch", ctypes.c_int64), ("seq_q", ctypes.c_int64),
+        ("seq_k", ctypes.c_int64), ("num_heads", ctypes.c_int64), ("head_dim", ctypes.c_int64),
+        ("q_strides", ctypes.c_int64 * 3), ("k_strides", ctypes.c_int64 * 3),
+        ("v_strides", ctypes.c_int64 * 3), ("scale", ctypes.c_float), ("causal", ctypes.c_int32),
+        ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
+EXPORTS = ("ca_store", "ca_decode", "ca_decode_workspace_bytes", "ca_flash",
+           "ca_flash_workspace_bytes", "ca_abi_version", "ca_version", "ca_status_string")
+
+_HOST_CHECKS = [os.environ.get("CPU_ATTENTION_HOST_CHECKS", "1") != "0"]
+
+
+def set_host_checks(enabled):
+    """Check slots and lengths against the cache on the host (the reference's
+    ValueErrors; a device sync per call when they live on the GPU). Returns the
+    previous setting."""
+    old = _HOST_CHECKS[0]
+    _HOST_CHECKS[0] = bool(enabled)
+    return old
+
+
+def host_checks():
+    return _HOST_CHECKS[0]
+
+
+def library_path():
+    return os.environ.get("CPU_ATTENTION_LIB") or os.path.join(_DIR, LIBRARY)
+
+
+def load_library(path=None):
+    """The ctypes handle of the kernel library, with every entry's signature set."""
+    lib = ctypes.CDLL(path or library_path())
+    vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+    lib.ca_store.argtypes = [ctypes.POINTER(StoreArgs), vp]
+    lib.ca_store.restype = ctypes.c_int
+    lib.ca_decode.argtypes = [ctypes.POINTER(DecodeArgs), vp]
+    lib.ca_decode.restype = ctypes.c_int
+    lib.ca_decode_workspace_bytes.argtypes = [i64, i64, i64, i64, i64]
+    lib.ca_decode_workspace_bytes.restype = i64
+    lib.ca_flash.argtypes = [ctypes.POINTER(FlashArgs), vp]
+    lib.ca_flash.restype = ctypes.c_int
+    lib.ca_flash_workspace_bytes.argtypes = [i64, i64, i64, i64, i64, i32]
+    lib.ca_flash_workspace_bytes.restype = i64
+    lib.ca_abi_version.argtypes = []
+    lib.ca_abi_version.restype = ctypes.c_int
+    lib.ca_version.argtypes = []
+    lib.ca_version.restype = ctypes.c_char_p
+    lib.ca_status_string.argtypes = [ctypes.c_int]
+    lib.ca_status_string.restype = ctypes.c_char_p
+    if lib.ca_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"cpu_attention: {path or library_path()} has ABI "
+                           f"{lib.ca_abi_version()}, this package needs {ABI_VERSION}")
+    return lib
+
+
+# ---------------------------------------------------------------------------
+# tensor helpers
+# ---------------------------------------------------------------------------
+def _plain(x):
+    return type(x) in _PLAIN
+
+
+def _stride(t, i):
+    """Stride of dim i, 0 for a dim of size 1 (never stepped over)."""
+    return 0 if t.shape[i] == 1 else t.stride(i)
+
+
+def _rows_ok(t, hd):
+    """Heads and dims contiguous (any token stride: chunks of a fused projection)."""
+    return t.stride(-1) == 1 and (t.shape[-2] == 1 or t.stride(-2) == hd)
+
+
+def aligned(t, strides=()):
+    """The kernels read 16-byte vectors: the data pointer and the given element
+    strides must keep 16-byte alignment."""
+    e = _ESIZE.get(t.dtype, 1)
+    return t.data_ptr() % 16 == 0 and all((s * e) % 16 == 0 for s in strides)
+
+
+def _on_gpu(device, *ts):
+    return all(t.is_cuda and t.device == device for t in ts)
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _caches_ok(kc, vc, dtype, heads, hd):
+    """``[blocks, heads, page, dim]``, contiguous, matching, page a multiple of 16
+    (the reference's _caches_ok, _C.mojo:74-80)."""
+    if not (_plain(kc) and _plain(vc)) or kc.dim() != 4 or vc.shape != kc.shape:
+        return False
+    return (kc.dtype == dtype and vc.dtype == dtype and kc.shape[1] == heads
+            and kc.shape[3] == hd and kc.shape[2] > 0 and kc.shape[2] % 16 == 0
+            and kc.is_contiguous() and vc.is_contiguous())
+
+
+def _int_vector(t, dtype, n):
+    return _plain(t) and t.dim() == 1 and t.dtype == dtype and t.shape[0] == n and t.is_contiguous()
+
+
+def _index_on(t, device):
+    """An index tensor on the kernels' device (CPU index tensors are copied over)."""
+    return t if t.device == device else t.to(device, non_blocking=True)
+
+
+class Module:
+    """The kernel module: the reference's ``decode``/``store``/``flash`` entries
+    over the C ABI of the gfx950 library."""
+
+    def __init__(self, lib):
+        self.lib = lib
+
+    def _raise(self, rc, what):
+        msg = self.lib.ca_status_string(rc).decode()
+        raise RuntimeError(f"cpu_attention: {what} failed on the GPU: {msg}")
+
+    def tier(self):
+        return "gfx950"
+
+    def amx_available(self):
+        return False
+
+    def version(self):
+        return self.lib.ca_version().decode()
+
+    # -- decode ---------------------------------------------------------------
+    def decode(self, rt, q, k_cache, v_cache, k, v, slots, lens, page_table, scale, dst):
+        """Paged decode of q ``[seqs, (1,) heads, dim]`` (MHA); see _C.mojo:87-171.
+        With k/v, each sequence's new token is stored first: at ``slots`` (then
+        ``lens`` is the length after the store), or appended at ``lens`` (the
+        length before). Writes ``dst`` when given, else a new tensor; returns it,
+        or None for anything the kernels do not take."""
+        if not (_plain(q) and _plain(page_table) and isinstance(lens, torch.Tensor)):
+            return None
+        nd = q.dim()
+        if nd not in (3, 4) or (nd == 4 and q.shape[1] != 1):
+            return None
+        b, heads, hd = q.shape[0], q.shape[-2], q.shape[-1]
+        if q.dtype not in DTYPES or hd not in HEAD_DIMS or not _rows_ok(q, hd):
+            return None
+        if not _caches_ok(k_cache, v_cache, q.dtype, heads, hd):
+            return None
+        page = k_cache.shape[2]
+        if page_table.dim() != 2 or page_table.dtype != torch.int32 or page_table.shape[0] != b \
+                or not page_table.is_contiguous():
+            return None
+        width = page_table.shape[1]
+        if not _int_vector(lens, torch.int32, b):
+            return None
+        store = k is not None
+        if store:
+            if not (_plain(k) and _plain(v) and k.shape == q.shape and v.shape == q.shape
+                    and v.stride() == k.stride()):
+                return None
+            if k.dtype != q.dtype or v.dtype != q.dtype or not _rows_ok(k, hd):
+                return None
+        elif v is not None:
+            return None
+        if slots is not None and not (store and _int_vector(slots, torch.int64, b)):
+            return None
+        dev = q.device
+        if not q.is_cuda or not _on_gpu(dev, k_cache, v_cache) or (store and not _on_gpu(dev, k, v)):
+            return None
+        if dst is not None and not (_plain(dst) and dst.shape == q.shape and dst.dtype == q.dtype
+                                    and dst.is_contiguous() and _on_gpu(dev, dst)):
+            return None
+        q_stride = _stride(q, 0)
+        kv_stride = _stride(k, 0) if store else 0
+        if not (aligned(q, (q_stride,)) and aligned(k_cache) and aligned(v_cache)):
+            return None
+        if store and not (aligned(k, (kv_stride,)) and aligned(v, (kv_stride,))):
+            return None
+        nblocks = k_cache.shape[0]
+        # The data-dependent rules (_C.mojo:139-153), on the host.
+        if _HOST_CHECKS[0] and b:
+            if slots is not None and int(slots.max()) >= nblocks * page:
+                return None
+            if int(lens.max()) + (1 if store and slots is None else 0) > width * page:
+                return None
+        lens = _index_on(lens, dev)
+        page_table = _index_on(page_table, dev)
+        if slots is not None:
+            slots = _index_on(slots, dev)
+        out = dst if dst is not None else torch.empty(q.shape, dtype=q.dtype, device=dev)
+        ws_bytes = self.lib.ca_decode_workspace_bytes(b, heads, hd, page, width)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        args = DecodeArgs(
+            q=q.data_ptr(), q_stride=q_stride, k_cache=k_cache.data_ptr(),
+            v_cache=v_cache.data_ptr(), k_new=k.data_ptr() if store else None,
+            v_new=v.data_ptr() if store else None, kv_stride=kv_stride,
+            slots=slots.data_ptr() if slots is not None else None, lens=lens.data_ptr(),
+            page_table=page_table.data_ptr(), page_table_width=width, out=out.data_ptr(),
+            num_seqs=b, num_heads=heads, head_dim=hd, page_size=page, num_blocks=nblocks,
+            scale=float(hd) ** -0.5 if scale is None else float(scale), dtype=DTYPES[q.dtype],
+            workspace=ws.data_ptr(), workspace_bytes=ws.numel())
+        rc = self.lib.ca_decode(ctypes.byref(args), _stream(dev))
+        if rc == CA_DECLINED:
+            return None
+        if rc != CA_OK:
+            self._raise(rc, "decode")
+        return out
+
+    # -- store ----------------------------------------------------------------
+    def store(self, rt, key, value, k_cache, v_cache, slots):
+        """``reshape_and_cache``: token i of key/value ``[tokens, heads, dim]`` goes
+        to slot ``slots[i]`` (int64; negative skips it). True, or None
+        (_C.mojo:174-213)."""
+        if not (isinstance(key, torch.Tensor) and isinstance(value, torch.Tensor)
+                and isinstance(slots, torch.Tensor)):
+            return None
+        if not (_plain(key) and _plain(value)) or key.dim() != 3 or value.dim() != 3:
+            return None
+        n, heads, hd = key.shape
+        if key.dtype not in DTYPES or hd not in HEAD_DIMS or value.dtype != key.dtype \
+                or not _rows_ok(key, hd):
+            return None
+        if value.shape != key.shape or value.stride() != key.stride():
+            return None
+        if not _caches_ok(k_cache, v_cache, key.dtype, heads, hd) \
+                or not _int_vector(slots, torch.int64, n):
+            return None
+        dev = k_cache.device
+        if not k_cache.is_cuda or not _on_gpu(dev, v_cache, key, value):
+            return None
+        tstride = _stride(key, 0)
+        if not (aligned(key, (tstride,)) and aligned(value) and aligned(k_cache)
+                and aligned(v_cache)):
+            return None
+        page, nblocks = k_cache.shape[2], k_cache.shape[0]
+        if _HOST_CHECKS[0] and n and int(slots.max()) >= nblocks * page:
+            return None
+        if n == 0:
+            return True
+        slots = _index_on(slots, dev)
+        args = StoreArgs(
+            key=key.data_ptr(), value=value.data_ptr(), token_stride=tstride,
+            k_cache=k_cache.data_ptr(), v_cache=v_cache.data_ptr(), slot_mapping=slots.data_ptr(),
+            num_tokens=n, num_heads=heads, head_dim=hd, page_size=page, num_blocks=nblocks,
+            dtype=DTYPES[key.dtype])
+        rc = self.lib.ca_store(ctypes.byref(args), _stream(dev))
+        if rc == CA_DECLINED:
+            return None
+        if rc != CA_OK:
+            self._raise(rc, "store")
+        return True
+
+    # -- flash ----------------------------------------------------------------
+    def flash_workspace_bytes(self, q, k):
+        return self.lib.ca_flash_workspace_bytes(q.shape[0], q.shape[1], k.shape[1], q.shape[2],
+                                                 q.shape[3], DTYPES.get(q.dtype, 0))
+
+    def flash(self, rt, q, k, v, scale, causal, ws, ws_bytes):
+        """flash_attn_func over q/k/v ``[batch, seq, heads, dim]`` (MHA, dims
+        contiguous). Returns the output, the workspace bytes it needs when
+        ``ws_bytes`` is short (an int), or None (_C.mojo:232-316)."""
+        if not all(isinstance(x, torch.Tensor) and _plain(x) for x in (q, k, v)):
+            return None
+        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+            return None
+        b, sq, heads, hd = q.shape
+        sk = k.shape[1]
+        if q.dtype not in DTYPES or hd not in HEAD_DIMS or sq < 1 or sk < 1:
+            return None
+        if k.shape[0] != b or k.shape[2] != heads or k.shape[3] != hd or k.dtype != q.dtype \
+                or v.dtype != q.dtype:
+            return None
+        if v.shape != k.shape:
+            return None
+        if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1:
+            return None
+        if not (causal is True or causal is False):
+            return None
+        dev = q.device
+        if not q.is_cuda or not _on_gpu(dev, k, v):
+            return None
+        qs, ks, vs = ([_stride(x, i) for i in range(3)] for x in (q, k, v))
+        if not (aligned(q, qs) and aligned(k, ks) and aligned(v, vs)):
+            return None
+        need = self.flash_workspace_bytes(q, k)
+        if need > ws_bytes:
+            return int(need)
+        out = torch.empty((b, sq, heads, hd), dtype=q.dtype, device=dev)
+        args = FlashArgs(
+            q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), out=out.data_ptr(), batch=b,
+            seq_q=sq, seq_k=sk, num_heads=heads, head_dim=hd,
+            q_strides=(ctypes.c_int64 * 3)(*qs), k_strides=(ctypes.c_int64 * 3)(*ks),
+            v_strides=(ctypes.c_int64 * 3)(*vs),
+            scale=float(hd) ** -0.5 if scale is None else float(scale),
+            causal=1 if causal else 0, dtype=DTYPES[q.dtype], workspace=ws or None,
+            workspace_bytes=ws_bytes)
+        rc = self.lib.ca_flash(ctypes.byref(args), _stream(dev))
+        if rc == CA_DECLINED:
+            return None
+        if rc != CA_OK:
+            self._raise(rc, "flash")
+        return out
+
+
+_MODULE = None
+_LOCK = threading.Lock()
+
+
+def module():
+    """The kernel module (RuntimeError when the library is not built)."""
+    global _MODULE
+    if _MODULE is None:
+        with _LOCK:
+            if _MODULE is None:
+                path = library_path()
+                if not os.path.exists(path):
+                    raise RuntimeError("cpu_attention: the gfx950 kernel library is not built; run "
+                                       "`python cpu-attention_amd/build.py`")
+                _MODULE = Module(load_library(path))
+    return _MODULE
+
+
+def runtime():
+    """An opaque handle the entries take as their first argument (the reference
+    passes its runtime-config address here, _kernel.py:167-207; the GPU build
+    keeps no runtime state)."""
+    module()
+    return ABI_VERSION
+
+
+def _cached(fn):
+    value = []
+    return lambda: value[0] if value else value.append(fn()) or value[0]
+
+
+@_cached
+def physical_cores():
+    """Physical cores visible to this process, from the sysfs topology."""
+    cores = set()
+    try:
+        for cpu in range(os.cpu_count() or 1):
+            base = f"/sys/devices/system/cpu/cpu{cpu}/topology"
+            with open(f"{base}/core_id") as f, open(f"{base}/physical_package_id") as g:
+                cores.add((g.read().strip(), f.read().strip()))
+    except OSError:
+        cores = set()
+    return len(cores) or (os.cpu_count() or 1)
+
+
+@_cached
+def llc_bytes():
+    """Last-level cache size of the host, from sysfs (32 MiB if unknown)."""
+    for idx in (3, 2, 1, 0):
+        try:
+            with open(f"/sys/devices/system/cpu/cpu0/cache/index{idx}/size") as f:
+                text = f.read().strip()
+        except OSError:
+            continue
+        unit = {"K": 1 << 10, "M": 1 << 20}.get(text[-1], 1)
+        return int(text.rstrip("KM")) * unit
+    return 32 << 20
+
+
+_WS = threading.local()
+
+
+def workspace(nbytes=0):
+    """This thread's flash workspace on the current GPU as (address, bytes), grown
+    to ``nbytes`` and never shrunk; (0, 0) until something asks for one."""
+    ws = getattr(_WS, "t", None)
+    if nbytes and (ws is None or ws.numel() < nbytes or ws.device.index != torch.cuda.current_device()):
+        _WS.t = ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    if ws is None:
+        return 0, 0
+    return ws.data_ptr(), ws.numel()

@@ -1,0 +1,173 @@
+// The extern "C" entries declared in include/cpu_attention_hip.h.  Each one checks
+// what its kernels assume (the static half of the reference's native validation,
+// cpu_attention/_mojo/src/_C.mojo:104-160, 190-205, 249-267, plus the 16-byte
+// alignment the vector loads need) and returns CA_DECLINED without launching
+// anything otherwise.
+#include <stdio.h>
+
+#include "ca_device.h"
+#include "ca_internal.h"
+
+using namespace ca;
+
+namespace {
+
+bool head_dim_ok(int64_t e) { return e == 32 || e == 64 || e == 128; }
+bool dtype_ok(int32_t dt) { return dt == CA_F32 || dt == CA_BF16; }
+int64_t esize(int32_t dt) { return dt == CA_BF16 ? 2 : 4; }
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+// An element stride whose byte size keeps 16-byte alignment.
+bool stride16(int64_t stride, int32_t dt) { return (stride * esize(dt)) % 16 == 0; }
+bool page_ok(int64_t page) { return page > 0 && page % 16 == 0; }
+
+}  // namespace
+
+extern "C" int ca_abi_version(void) { return CA_ABI_VERSION; }
+
+extern "C" const char* ca_version(void) {
+  return "cpu-attention gfx950 (MI355X) HIP kernels, ABI " "1";
+}
+
+extern "C" const char* ca_status_string(int status) {
+  if (status == CA_OK) return "ok";
+  if (status == CA_DECLINED) return "declined: arguments outside what the kernels take";
+  if (status < 0) return hipGetErrorString((hipError_t)(CA_HIP_ERROR - status));
+  return "unknown status";
+}
+
+extern "C" int ca_store(const ca_store_args* a, void* stream) {
+  if (!a || !dtype_ok(a->dtype) || !head_dim_ok(a->head_dim) || !page_ok(a->page_size))
+    return CA_DECLINED;
+  if (a->num_tokens < 0 || a->num_heads <= 0 || a->num_blocks < 0) return CA_DECLINED;
+  if (a->num_tokens == 0) return CA_OK;
+  if (!a->key || !a->value || !a->k_cache || !a->v_cache || !a->slot_mapping) return CA_DECLINED;
+  if (!aligned16(a->key) || !aligned16(a->value) || !aligned16(a->k_cache) ||
+      !aligned16(a->v_cache) || !stride16(a->token_stride, a->dtype) ||
+      a->token_stride < a->num_heads * a->head_dim)
+    return CA_DECLINED;
+  const int64_t words = a->head_dim * esize(a->dtype) / 4;
+  StoreParams p{};
+  p.key = static_cast<const uint32_t*>(a->key);
+  p.value = static_cast<const uint32_t*>(a->value);
+  p.tok_stride_w = a->token_stride * esize(a->dtype) / 4;
+  p.kc = static_cast<uint32_t*>(a->k_cache);
+  p.vc = static_cast<uint32_t*>(a->v_cache);
+  p.slots = a->slot_mapping;
+  p.ntok = a->num_tokens;
+  p.heads = a->num_heads;
+  p.page = a->page_size;
+  p.nblocks = a->num_blocks;
+  return store_launch(p, (int)words, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t ca_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads,
+                                             int64_t head_dim, int64_t page_size,
+                                             int64_t page_table_width) {
+  if (num_seqs < 0 || num_heads < 0 || page_size <= 0 || page_table_width < 0) return -1;
+  const int64_t tiles = decode_tiles(page_table_width, page_size);
+  // partial accumulators [N*H, tiles, E] then (max, sum) pairs [N*H, tiles, 2]
+  const int64_t acc = num_seqs * num_heads * tiles * head_dim * 4;
+  const int64_t ml = num_seqs * num_heads * tiles * 2 * 4;
+  return ((acc + 255) / 256) * 256 + ml;
+}
+
+extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
+  if (!a || !dtype_ok(a->dtype) || !head_dim_ok(a->head_dim) || !page_ok(a->page_size))
+    return CA_DECLINED;
+  if (a->num_seqs < 0 || a->num_heads <= 0 || a->num_blocks < 0 || a->page_table_width < 0)
+    return CA_DECLINED;
+  if (a->num_seqs == 0) return CA_OK;
+  if (!a->q || !a->k_cache || !a->v_cache || !a->lens || !a->page_table || !a->out)
+    return CA_DECLINED;
+  if ((a->k_new == nullptr) != (a->v_new == nullptr)) return CA_DECLINED;
+  if (a->slots && !a->k_new) return CA_DECLINED;
+  if (!aligned16(a->q) || !aligned16(a->k_cache) || !aligned16(a->v_cache) ||
+      !aligned16(a->out) || !stride16(a->q_stride, a->dtype))
+    return CA_DECLINED;
+  if (a->k_new && (!aligned16(a->k_new) || !aligned16(a->v_new) || !stride16(a->kv_stride, a->dtype)))
+    return CA_DECLINED;
+  const int64_t need = ca_decode_workspace_bytes(a->num_seqs, a->num_heads, a->head_dim,
+                                                 a->page_size, a->page_table_width);
+  if (!a->workspace || !aligned16(a->workspace) || a->workspace_bytes < need) return CA_DECLINED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t words = a->head_dim * esize(a->dtype) / 4;
+
+  // The new token first (the reference stores, then attends: paged_attn.mojo:852-863).
+  if (a->k_new) {
+    StoreParams sp{};
+    sp.key = static_cast<const uint32_t*>(a->k_new);
+    sp.value = static_cast<const uint32_t*>(a->v_new);
+    sp.tok_stride_w = a->kv_stride * esize(a->dtype) / 4;
+    sp.kc = static_cast<uint32_t*>(a->k_cache);
+    sp.vc = static_cast<uint32_t*>(a->v_cache);
+    sp.slots = a->slots;
+    sp.lens = a->lens;
+    sp.page_table = a->page_table;
+    sp.pt_width = a->page_table_width;
+    sp.ntok = a->num_seqs;
+    sp.heads = a->num_heads;
+    sp.page = a->page_size;
+    sp.nblocks = a->num_blocks;
+    const int r = store_launch(sp, (int)words, st);
+    if (r != CA_OK) return r;
+  }
+
+  DecodeParams p{};
+  p.q = a->q;
+  p.q_stride = a->q_stride;
+  p.kc = static_cast<const uint32_t*>(a->k_cache);
+  p.vc = a->v_cache;
+  p.lens = a->lens;
+  // Appending at lens: the row attends lens + 1 keys.  With slots, lens is
+  // already the post-store length (_C.mojo:100-103, paged_attn.mojo:721-723).
+  p.len_add = (a->k_new && !a->slots) ? 1 : 0;
+  p.page_table = a->page_table;
+  p.pt_width = a->page_table_width;
+  p.heads = a->num_heads;
+  p.page = a->page_size;
+  p.nblocks = a->num_blocks;
+  p.nseqs = a->num_seqs;
+  p.c = a->scale * kLog2e;
+  p.tiles = (int)decode_tiles(a->page_table_width, a->page_size);
+  const int64_t acc_bytes =
+      ((a->num_seqs * a->num_heads * p.tiles * a->head_dim * 4 + 255) / 256) * 256;
+  p.part_acc = static_cast<float*>(a->workspace);
+  p.part_ml = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + acc_bytes);
+  p.out = a->out;
+  return decode_launch(p, (int)a->head_dim, a->dtype == CA_BF16, st);
+}
+
+extern "C" int64_t ca_flash_workspace_bytes(int64_t, int64_t, int64_t, int64_t, int64_t,
+                                            int32_t) {
+  return 0;
+}
+
+extern "C" int ca_flash(const ca_flash_args* a, void* stream) {
+  if (!a || !dtype_ok(a->dtype) || !head_dim_ok(a->head_dim)) return CA_DECLINED;
+  if (a->batch < 0 || a->num_heads <= 0 || a->seq_q < 1 || a->seq_k < 1) return CA_DECLINED;
+  if (a->batch == 0) return CA_OK;
+  if (!a->q || !a->k || !a->v || !a->out) return CA_DECLINED;
+  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->out))
+    return CA_DECLINED;
+  for (int i = 0; i < 3; ++i)
+    if (!stride16(a->q_strides[i], a->dtype) || !stride16(a->k_strides[i], a->dtype) ||
+        !stride16(a->v_strides[i], a->dtype))
+      return CA_DECLINED;
+  FlashParams p{};
+  p.q = a->q;
+  p.k = a->k;
+  p.v = a->v;
+  p.out = a->out;
+  p.batch = a->batch;
+  p.seq_q = a->seq_q;
+  p.seq_k = a->seq_k;
+  p.heads = a->num_heads;
+  for (int i = 0; i < 3; ++i) {
+    p.qs[i] = a->q_strides[i];
+    p.ks[i] = a->k_strides[i];
+    p.vs[i] = a->v_strides[i];
+  }
+  p.c = a->scale * kLog2e;
+  p.causal = a->causal ? 1 : 0;
+  return flash_launch(p, (int)a->head_dim, a->dtype == CA_BF16, static_cast<hipStream_t>(stream));
+}

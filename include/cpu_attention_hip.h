@@ -1,0 +1,162 @@
+/*
+ * cpu_attention_hip.h -- the C ABI of the gfx950 (MI355X) build of cpu-attention's
+ * three ops: reshape_and_cache, paged decode (flash_attn_with_kvcache) and dense
+ * prefill (flash_attn_func).
+ *
+ * Every entry takes plain device pointers, element counts and element strides (no
+ * torch types), validates what it can see without reading device memory, enqueues
+ * its kernels on `stream` (a hipStream_t; NULL = the legacy default stream) and
+ * returns without synchronising.
+ *
+ * Return codes:
+ *   CA_OK (0)        the kernels were enqueued;
+ *   CA_DECLINED (1)  the arguments are outside what the kernels take (shape,
+ *                    dtype, head_dim, page size, alignment, workspace): nothing
+ *                    was enqueued.  The Python layer turns this into the
+ *                    reference's ValueError / NotImplementedError, or copies the
+ *                    operands to a readable layout and calls again;
+ *   CA_HIP_ERROR (<0) a HIP launch error; ca_status_string() names it.
+ *
+ * The entries are re-entrant and keep no global mutable state.  None allocates:
+ * outputs and split-K scratch are passed in by the caller.
+ *
+ * Data-dependent bounds (a slot past the cache's end, a length beyond the page
+ * table's capacity, a page-table entry that names no block) are guarded inside
+ * the kernels: such a token is not stored, such a position is not read.  The
+ * reference raises ValueError for the first two; the Python layer does that
+ * check on the host before calling (see cpu_attention/_kernel.py).
+ *
+ * Cache layout (the reference's PageLayout, cpu_attention/_mojo/src/paged_attn.mojo:58-130,
+ * x86 mapping): k_cache and v_cache are [num_blocks, num_heads, page_size, head_dim],
+ * contiguous.  Block (b, h) starts at element (b*H + h)*P*E.  Within it:
+ *   fp32 K: element K[d][t]  at  d*P + t;
+ *   bf16 K: 32-bit words [E/2][P]; word (d2, t) holds the bf16 pair
+ *           (K[2*d2], K[2*d2+1]), i.e. element (d2*P + t)*2 + (d & 1);
+ *   V (both dtypes): rows [P][E], element t*E + d.
+ */
+#ifndef CPU_ATTENTION_HIP_H
+#define CPU_ATTENTION_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CA_ABI_VERSION 1
+
+enum { CA_F32 = 0, CA_BF16 = 1 };
+
+enum { CA_OK = 0, CA_DECLINED = 1, CA_HIP_ERROR = -1 };
+
+/* reshape_and_cache (cpu_attention/cache.py:13-25, native entry `store`
+ * cpu_attention/_mojo/src/_C.mojo:174-213).  Token i of key/value
+ * [num_tokens, num_heads, head_dim] (heads and dims contiguous, any token
+ * stride, the same for both) goes to slot s = slot_mapping[i]: block s / P,
+ * position s % P.  s < 0 skips the token; s >= num_blocks*P is not stored. */
+typedef struct ca_store_args {
+  const void* key;
+  const void* value;
+  int64_t token_stride;  /* elements between consecutive tokens of key/value */
+  void* k_cache;
+  void* v_cache;
+  const int64_t* slot_mapping;  /* [num_tokens], int64 */
+  int64_t num_tokens;
+  int64_t num_heads;
+  int64_t head_dim;   /* 32, 64 or 128 */
+  int64_t page_size;  /* a positive multiple of 16 */
+  int64_t num_blocks;
+  int32_t dtype;      /* CA_F32 or CA_BF16 */
+  int32_t reserved;
+} ca_store_args;
+
+int ca_store(const ca_store_args* args, void* stream);
+
+/* Paged decode (flash_attn_interface.py:37-127, native entry `decode`
+ * _C.mojo:87-171): one query row per (sequence, head) against the sequence's
+ * cached K/V, online softmax in base 2, fp32 accumulation, output in the input
+ * dtype; a row with no key is exactly 0.
+ *
+ * With k_new/v_new (one token per sequence) the token is stored first:
+ *   slots == NULL: at position lens[s] through page_table (lens is the length
+ *                  before the store; the row attends lens[s] + 1 keys;
+ *                  lens[s] < 0 stores nothing);
+ *   slots != NULL: at slot slots[s] (negative skips), and lens[s] is the
+ *                  length after the store (the engine path, examples/ops.py:19-25).
+ * Without k_new/v_new the row attends lens[s] keys.
+ *
+ * q, k_new, v_new: [num_seqs, num_heads, head_dim] rows, heads and dims
+ * contiguous, sequence stride q_stride / kv_stride (elements).
+ * out: [num_seqs, num_heads, head_dim] contiguous.
+ * workspace: at least ca_decode_workspace_bytes(...) bytes of device memory,
+ * 256-byte aligned; its contents need not be initialised. */
+typedef struct ca_decode_args {
+  const void* q;
+  int64_t q_stride;
+  void* k_cache;
+  void* v_cache;
+  const void* k_new;   /* NULL: no store */
+  const void* v_new;
+  int64_t kv_stride;
+  const int64_t* slots;      /* NULL or [num_seqs] int64 */
+  const int32_t* lens;       /* [num_seqs] int32 */
+  const int32_t* page_table; /* [num_seqs, page_table_width] int32, contiguous */
+  int64_t page_table_width;
+  void* out;
+  int64_t num_seqs;
+  int64_t num_heads;
+  int64_t head_dim;
+  int64_t page_size;
+  int64_t num_blocks;
+  float scale;        /* softmax scale (the caller resolves the 1/sqrt(E) default) */
+  int32_t dtype;
+  void* workspace;
+  int64_t workspace_bytes;
+} ca_decode_args;
+
+int64_t ca_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t head_dim,
+                                  int64_t page_size, int64_t page_table_width);
+int ca_decode(const ca_decode_args* args, void* stream);
+
+/* Dense prefill (flash_attn_interface.py:168-193, native entry `flash`
+ * _C.mojo:232-316).  q [batch, seq_q, H, E], k/v [batch, seq_k, H, E] with any
+ * batch/token/head strides (elements; the head_dim stride is 1).  Causal is
+ * bottom-right aligned: query i sees keys j <= i + seq_k - seq_q; a row that sees
+ * no key is exactly 0.  out is a contiguous [batch, seq_q, H, E] in the input
+ * dtype.  The workspace is used only by the few-query-rows route; pass the bytes
+ * ca_flash_workspace_bytes() asks for (0 means none is needed). */
+typedef struct ca_flash_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int64_t batch;
+  int64_t seq_q;
+  int64_t seq_k;
+  int64_t num_heads;
+  int64_t head_dim;
+  int64_t q_strides[3];  /* batch, token, head */
+  int64_t k_strides[3];
+  int64_t v_strides[3];
+  float scale;
+  int32_t causal;
+  int32_t dtype;
+  int32_t reserved;
+  void* workspace;
+  int64_t workspace_bytes;
+} ca_flash_args;
+
+int64_t ca_flash_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k,
+                                 int64_t num_heads, int64_t head_dim, int32_t dtype);
+int ca_flash(const ca_flash_args* args, void* stream);
+
+/* ABI version (CA_ABI_VERSION), a build description, and a readable status. */
+int ca_abi_version(void);
+const char* ca_version(void);
+const char* ca_status_string(int status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CPU_ATTENTION_HIP_H */

@@ -1,0 +1,105 @@
+"""The C ABI library: it loads, exports every entry include/*.h declares, its ctypes
+structures match the C header byte for byte, and it declines malformed calls
+without touching a GPU (CPU only)."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from cpu_attention import _kernel as K
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cpu_attention_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*[\w\s\*]+?\b(ca_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_entry():
+    names = declared_functions()
+    assert {"ca_store", "ca_decode", "ca_flash", "ca_version"} <= set(names)
+    lib = ctypes.CDLL(K.library_path())
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(K.EXPORTS) == set(names)
+
+
+def test_version_and_status_strings():
+    lib = K.load_library()
+    assert lib.ca_abi_version() == K.ABI_VERSION == 1
+    assert b"gfx950" in lib.ca_version()
+    assert lib.ca_status_string(0) == b"ok"
+    assert b"declined" in lib.ca_status_string(1)
+    assert lib.ca_status_string(-1 - 1)  # a HIP error code renders as text
+
+
+_LAYOUT_C = r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "cpu_attention_hip.h"
+#define F(T, f) printf("%s.%s %zu %zu\n", #T, #f, offsetof(T, f), sizeof(((T*)0)->f));
+int main(void) {
+  printf("ca_store_args %zu\n", sizeof(ca_store_args));
+  printf("ca_decode_args %zu\n", sizeof(ca_decode_args));
+  printf("ca_flash_args %zu\n", sizeof(ca_flash_args));
+  FIELDS
+  return 0;
+}
+"""
+
+
+def test_ctypes_structures_match_the_header():
+    structs = {"ca_store_args": K.StoreArgs, "ca_decode_args": K.DecodeArgs,
+               "ca_flash_args": K.FlashArgs}
+    fields = "\n".join(f"F({c}, {name})" for c, py in structs.items() for name, _ in py._fields_)
+    with tempfile.TemporaryDirectory() as d:
+        src, exe = os.path.join(d, "layout.c"), os.path.join(d, "layout")
+        open(src, "w").write(_LAYOUT_C.replace("FIELDS", fields))
+        subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), src, "-o", exe],
+                       check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n")
+    for line in filter(None, out):
+        parts = line.split()
+        if len(parts) == 2:
+            assert ctypes.sizeof(structs[parts[0]]) == int(parts[1]), line
+        else:
+            cname, field = parts[0].split(".")
+            desc = getattr(structs[cname], field)
+            assert (desc.offset, desc.size) == (int(parts[1]), int(parts[2])), line
+
+
+def test_entries_decline_malformed_calls_without_a_gpu():
+    lib = K.load_library()
+    s = K.StoreArgs(num_tokens=4, num_heads=2, head_dim=48, page_size=16, dtype=0)
+    assert lib.ca_store(ctypes.byref(s), None) == K.CA_DECLINED  # head_dim
+    s.head_dim, s.page_size = 64, 24
+    assert lib.ca_store(ctypes.byref(s), None) == K.CA_DECLINED  # page
+    s.page_size = 16
+    assert lib.ca_store(ctypes.byref(s), None) == K.CA_DECLINED  # null pointers
+    s.num_tokens = 0
+    assert lib.ca_store(ctypes.byref(s), None) == K.CA_OK  # nothing to do
+    d = K.DecodeArgs(num_seqs=2, num_heads=2, head_dim=64, page_size=16, dtype=3)
+    assert lib.ca_decode(ctypes.byref(d), None) == K.CA_DECLINED  # dtype
+    d.dtype = 1
+    assert lib.ca_decode(ctypes.byref(d), None) == K.CA_DECLINED  # null pointers
+    f = K.FlashArgs(batch=1, seq_q=0, seq_k=4, num_heads=1, head_dim=64, dtype=1)
+    assert lib.ca_flash(ctypes.byref(f), None) == K.CA_DECLINED  # seq_q < 1
+    f.seq_q = 4
+    assert lib.ca_flash(ctypes.byref(f), None) == K.CA_DECLINED  # null pointers
+    assert lib.ca_decode_workspace_bytes(64, 32, 128, 32, 64) == \
+        ((64 * 32 * 8 * 128 * 4 + 255) // 256) * 256 + 64 * 32 * 8 * 2 * 4
+    assert lib.ca_flash_workspace_bytes(1, 1, 1, 1, 64, 1) == 0
+
+
+def test_missing_library_is_a_loud_error(monkeypatch):
+    monkeypatch.setenv("CPU_ATTENTION_LIB", "/nonexistent/libcpu_attention_hip.so")
+    monkeypatch.setattr(K, "_MODULE", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        K.module()

@@ -1,0 +1,127 @@
+"""flash_attn_func on the GPU against the float64 oracle.  Mirrors the reference's
+tests/test_flash.py case for case (shape grid with tile edges and unequal lengths,
+batch and scale, fused-qkv strides, fuzz, repeated calls), then adds the
+BASELINE prefill shapes, rows with no visible key, and layouts that need a copy."""
+
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from cpu_attention import flash_attn_func
+from helpers import assert_close, attention, values
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.float32, torch.bfloat16]
+# (seq_q, seq_k): tile edges (16/64/128 rows), single rows, unequal lengths both ways.
+LENGTHS = [(1, 1), (17, 17), (64, 64), (129, 129), (1, 300), (100, 37), (37, 100), (257, 513)]
+
+
+def run(b, sq, sk, h, d, dtype, causal, seed, device, scale=None):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(b, n, h, d, generator=g).to(dtype).to(device) for n in (sq, sk, sk))
+    out = flash_attn_func(q, k, v, softmax_scale=scale, causal=causal)
+    assert out.shape == q.shape and out.dtype == dtype and out.is_contiguous()
+    ref = attention(values(q), values(k), values(v), scale or d ** -0.5, causal)
+    assert_close(out, ref, dtype, paged=False)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("sq,sk", LENGTHS)
+@pytest.mark.parametrize("h", [1, 8])
+@pytest.mark.parametrize("causal", [True, False])
+def test_shapes(cuda, dtype, d, sq, sk, h, causal):
+    run(1, sq, sk, h, d, dtype, causal, seed=sq * 1000 + sk, device=cuda)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_batch_and_scale(cuda, dtype):
+    run(3, 70, 150, 8, 64, dtype, True, seed=1, device=cuda, scale=0.07)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_fused_qkv_strides(cuda, dtype):
+    """q/k/v as chunks of one [b, s, 3*h*d] projection (no copy is needed)."""
+    b, s, h, d = 2, 200, 4, 64
+    qkv = torch.randn(b, s, 3 * h * d).to(dtype).to(cuda)
+    q, k, v = (qkv[..., i * h * d:(i + 1) * h * d].view(b, s, h, d) for i in range(3))
+    out = flash_attn_func(q, k, v, causal=True)
+    assert_close(out, attention(values(q), values(k), values(v), d ** -0.5, True), dtype, paged=False)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_fuzz(cuda, seed):
+    r = random.Random(seed)
+    run(r.randint(1, 3), r.randint(1, 900), r.randint(1, 900), r.choice([1, 4, 12]),
+        r.choice([32, 64, 128]), r.choice(DTYPES), r.random() < 0.5, seed, cuda)
+
+
+def test_repeated_calls_follow_changes(cuda):
+    """The call plan must follow every change of scale, causal and shape."""
+    for scale, causal, s in ((0.05, True, 64), (0.125, False, 64), (0.05, False, 65)):
+        run(1, s, s, 4, 64, torch.float32, causal, seed=s, device=cuda, scale=scale)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_rows_without_keys_are_zero(cuda, dtype):
+    """Causal with seq_q > seq_k: the first seq_q - seq_k rows see no key and are 0."""
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(2, 300, 4, 64, generator=g).to(dtype).to(cuda)
+    k = torch.randn(2, 90, 4, 64, generator=g).to(dtype).to(cuda)
+    out = flash_attn_func(q, k, k, causal=True)
+    assert torch.count_nonzero(out[:, :210]) == 0
+    assert_close(out, attention(values(q), values(k), values(k), 64 ** -0.5, True), dtype, paged=False)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_layouts_needing_a_copy(cuda, dtype):
+    """A head dim that is not contiguous, and a 16-byte-misaligned view, are copied
+    by the Python layer and still computed correctly."""
+    g = torch.Generator().manual_seed(3)
+    base = torch.randn(1, 50, 4, 130, generator=g).to(dtype).to(cuda)
+    q = base[..., 1:65]  # misaligned start, token/head strides not 16-byte multiples
+    k = torch.randn(1, 64, 50, 4, generator=g).to(dtype).to(cuda).permute(0, 2, 3, 1)  # dim stride != 1
+    v = torch.randn(1, 50, 4, 64, generator=g).to(dtype).to(cuda)
+    out = flash_attn_func(q, k, v, causal=False)
+    assert_close(out, attention(values(q), values(k), values(v), 64 ** -0.5), dtype, paged=False)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_north_star_tolerance_fp32(cuda, causal):
+    """fp32 within 1e-5 relative of float64 (the north-star gate), longer rows."""
+    run(1, 1000, 1000, 2, 128, torch.float32, causal, seed=5, device=cuda)
+
+
+def test_cfg1_prefill_bf16(cuda):
+    """N=1 L=S=128 H=16 E=64 causal bottom-right, bf16."""
+    run(1, 128, 128, 16, 64, torch.bfloat16, True, seed=0, device=cuda)
+
+
+def test_cfg4_cross_shape(cuda):
+    """BASELINE config 3 (cross shape): N=8 L=1 S=2048 E=32 H=32, non-causal, bf16."""
+    run(8, 1, 2048, 32, 32, torch.bfloat16, False, seed=8, device=cuda)
+
+
+def test_cfg4_prefill_full_size_sampled(cuda):
+    """N=4 L=S=4096 H=32 E=128 causal bf16, q/k/v strided chunks of a
+    fused [N*L, 3*H*E] projection.  The whole output is computed; the float64 oracle
+    checks sampled (batch, head) pairs on sampled rows (first, last, tile edges,
+    random)."""
+    N, L, H, E = 4, 4096, 32, 128
+    g = torch.Generator(device=cuda).manual_seed(4)
+    qkv = torch.randn(N * L, 3 * H * E, generator=g, device=cuda).to(torch.bfloat16)
+    q, k, v = (qkv[:, i * H * E:(i + 1) * H * E].view(N, L, H, E) for i in range(3))
+    out = flash_attn_func(q, k, v, causal=True)
+    assert torch.isfinite(out).all()
+    rows = np.array(sorted({0, 1, 127, 128, 129, 2047, 2048, 4094, 4095, *range(300, 4096, 613)}))
+    for b, h in ((0, 0), (1, 17), (3, 31)):
+        qs = values(q[b, rows, h])  # [r, E]
+        kb, vb = values(k[b, :, h]), values(v[b, :, h])
+        w = qs @ kb.T * E ** -0.5
+        w = np.where(np.arange(L)[None, :] > rows[:, None], -np.inf, w)
+        w = np.exp(w - w.max(-1, keepdims=True))
+        ref = (w / w.sum(-1, keepdims=True)) @ vb
+        got = values(out[b, rows, h])
+        assert np.abs(got - ref).max() <= 2e-2

@@ -1,0 +1,233 @@
+"""flash_attn_with_kvcache (paged decode), the append, and reshape_and_cache on the
+GPU against the float64 oracle and the layout oracle.  Mirrors the reference's
+tests/test_kvcache.py case for case, then adds byte-level cache checks, the
+engine entry (slots + out=), and the BASELINE decode shapes."""
+
+import random
+import threading
+
+import numpy as np
+import pytest
+import torch
+
+from cpu_attention import _kernel as K
+from cpu_attention import flash_attn_with_kvcache, reshape_and_cache
+from helpers import (NAME, appended, assert_close, cache_words, layout, reference, row_words,
+                     stage, values)
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+def decode(lens, h, d, page, dtype, seed, device, scale=None):
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed, device)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    out = flash_attn_with_kvcache(q, kc, vc, cache_seqlens=seqlens, page_table=bt,
+                                  softmax_scale=scale)
+    assert_close(out, reference(q, ks, vs, scale or d ** -0.5), dtype, paged=True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("page", [16, 32, 48, 64])
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("h", [1, 8])
+def test_decode(cuda, dtype, page, d, h):
+    decode([0, 1, page - 1, page, page + 1, 255, 257], h, d, page, dtype, seed=page + d, device=cuda)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_append_one_token(cuda, dtype):
+    """k/v of one new token are written at cache_seqlens and attended in the same call."""
+    lens, h, d = [5, 31, 64, 300], 8, 64
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, 16, dtype, seed=3, device=cuda)
+    kn, vn = (torch.randn(len(lens), 1, h, d).to(dtype).to(cuda) for _ in range(2))
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    out = flash_attn_with_kvcache(q, kc, vc, k=kn, v=vn, cache_seqlens=seqlens, page_table=bt)
+    ref = reference(q, *appended(ks, vs, kn, vn), d ** -0.5)
+    assert_close(out, ref, dtype, paged=True)
+    # flash-attn 2's name for the page table
+    again = flash_attn_with_kvcache(q, kc, vc, cache_seqlens=seqlens + 1, block_table=bt)
+    assert_close(again, ref, dtype, paged=True)
+
+
+@pytest.mark.parametrize("host_checks", [True, False])
+def test_uneven_lengths(cuda, host_checks):
+    """Lopsided batches (the reference sweeps thread counts here; the GPU splits every
+    row into 256-key tiles, so this sweeps the host-check mode instead)."""
+    old = K.set_host_checks(host_checks)
+    try:
+        for seed, lens in enumerate(([0, 2047, 1, 17, 64], [2047, 16], [5, 3, 1024])):
+            decode(lens, 8, 64, 16, torch.float32, seed=seed, device=cuda)
+    finally:
+        K.set_host_checks(old)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_fused_projection_strides(cuda, dtype):
+    """q and the new k/v as chunks of one fused [b, 1, 3 h d] projection."""
+    lens, h, d = [40, 200], 8, 64
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, 32, dtype, seed=4, device=cuda)
+    qkv = torch.randn(len(lens), 1, 3 * h * d).to(dtype).to(cuda)
+    qn, kn, vn = (qkv[..., i * h * d:(i + 1) * h * d].view(len(lens), 1, h, d) for i in range(3))
+    out = flash_attn_with_kvcache(qn, kc, vc, k=kn, v=vn, page_table=bt,
+                                  cache_seqlens=torch.tensor(lens, dtype=torch.int32, device=cuda))
+    assert_close(out, reference(qn, *appended(ks, vs, kn, vn), d ** -0.5), dtype, paged=True)
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_fuzz(cuda, seed):
+    r = random.Random(seed)
+    lens = [r.randint(0, 1100) for _ in range(r.randint(1, 6))]
+    d = r.choice([32, 64, 128])
+    decode(lens, r.choice([1, 4, 12]), d, r.choice([16, 32, 48, 64]), r.choice(DTYPES), seed,
+           cuda, scale=r.choice([1.0, 0.5]) * d ** -0.5)
+
+
+def test_concurrent_callers(cuda):
+    """Python threads calling at once each get their own correct result."""
+    cases = [stage([100 + 50 * i, 33], 8, 64, 16, torch.float32, seed=i, device=cuda) for i in range(4)]
+    refs = [reference(q, ks, vs, 0.125) for q, _, _, _, ks, vs in cases]
+    errors = []
+
+    def worker(i):
+        q, kc, vc, bt, _, _ = cases[i]
+        seqlens = torch.tensor([100 + 50 * i, 33], dtype=torch.int32, device=cuda)
+        for _ in range(20):
+            out = flash_attn_with_kvcache(q, kc, vc, cache_seqlens=seqlens, page_table=bt,
+                                          softmax_scale=0.125)
+            errors.append(float(np.abs(values(out) - refs[i]).max()))
+
+    pool = [threading.Thread(target=worker, args=(i,)) for i in range(4)]
+    for t in pool:
+        t.start()
+    for t in pool:
+        t.join()
+    assert len(errors) == 80 and max(errors) <= 1e-6
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("page", [16, 32])
+def test_reshape_and_cache(cuda, dtype, page):
+    """reshape_and_cache writes the same cache an append does (byte for byte);
+    negative slots skip, and k/v may be chunks of a fused projection."""
+    lens, h, d = [70, 5], 8, 64
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=6, device=cuda)
+    kc2, vc2 = torch.full_like(kc, float("nan")), torch.full_like(vc, float("nan"))
+    kv = torch.cat([torch.cat([k[0], v[0]], -1) for k, v in zip(ks, vs)])  # [tokens, h, 2d]
+    pos = torch.cat([torch.arange(n) for n in lens])
+    seq = torch.cat([torch.full((n,), i) for i, n in enumerate(lens)])
+    slots = bt.cpu()[seq, pos // page].long() * page + pos % page
+    kv = torch.cat([kv, torch.randn(3, h, 2 * d).to(dtype).to(cuda)])  # 3 padding tokens, slot -1
+    reshape_and_cache(kv[..., :d], kv[..., d:], kc2, vc2,
+                      torch.cat([slots, torch.full((3,), -1, dtype=torch.int64)]).to(cuda))
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    out = flash_attn_with_kvcache(q, kc2, vc2, cache_seqlens=seqlens, page_table=bt)
+    assert_close(out, reference(q, ks, vs, d ** -0.5), dtype, paged=True)
+    np.testing.assert_array_equal(cache_words(kc2), cache_words(kc))
+    np.testing.assert_array_equal(cache_words(vc2), cache_words(vc))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("page", [16, 48])
+@pytest.mark.parametrize("pattern", ["consecutive", "scattered", "unaligned_run"])
+def test_store_bit_exact(cuda, dtype, d, page, pattern):
+    """The store against the layout oracle, whole cache compared as bytes (unwritten
+    slots keep their NaN poison)."""
+    g = torch.Generator().manual_seed(d * page)
+    nb, h, T = 9, 3, 70
+    cap = nb * page
+    if pattern == "consecutive":
+        slots = torch.arange(page, page + T)
+    elif pattern == "scattered":
+        slots = torch.randperm(cap, generator=g)[:T]
+    else:
+        slots = torch.arange(5, 5 + T)  # runs that start mid-page and cross pages
+    slots = slots.clone()
+    slots[::7] = -1  # padding
+    # key/value as chunks of one fused [T, 3*h*d] projection: token stride 3*h*d
+    src = torch.randn(T, 3 * h * d, generator=g).to(dtype).to(cuda)
+    key, value = src[:, :h * d].view(T, h, d), src[:, 2 * h * d:].view(T, h, d)
+    kc = torch.full((nb, h, page, d), float("nan"), dtype=dtype, device=cuda)
+    vc = kc.clone()
+    reshape_and_cache(key, value, kc, vc, slots.to(cuda))
+    kw = cache_words(torch.full((nb, h, page, d), float("nan"), dtype=dtype))
+    vw = kw.copy()
+    layout.store(kw, vw, row_words(key), row_words(value), slots.numpy(), page)
+    np.testing.assert_array_equal(cache_words(kc), kw)
+    np.testing.assert_array_equal(cache_words(vc), vw)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_multi_token_append_bytes(cuda, dtype):
+    """The multi-token append (flash_attn_interface.py:109-117) writes what the
+    layout oracle's prompt slots say, then decodes over the grown cache."""
+    h, d, page = 4, 64, 32
+    nb = 12
+    g = torch.Generator().manual_seed(11)
+    table = torch.randperm(nb, generator=g)[:8].to(torch.int32).view(2, 4)
+    kc = torch.full((nb, h, page, d), float("nan"), dtype=dtype, device=cuda)
+    vc = kc.clone()
+    k = torch.randn(2, 50, h, d, generator=g).to(dtype).to(cuda)
+    v = torch.randn(2, 50, h, d, generator=g).to(dtype).to(cuda)
+    q = torch.randn(2, 1, h, d, generator=g).to(dtype).to(cuda)
+    start = torch.tensor([3, 40], dtype=torch.int32)
+    kw = cache_words(kc.cpu())
+    vw = kw.copy()
+    for i in range(2):
+        s = layout.prompt_slots(int(start[i]), 50, table[i].numpy(), page)
+        layout.store(kw, vw, row_words(k[i]), row_words(v[i]), s, page)
+    flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=start.to(cuda), page_table=table.to(cuda))
+    np.testing.assert_array_equal(cache_words(kc), kw)
+    np.testing.assert_array_equal(cache_words(vc), vw)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("q_rank", [3, 4])
+def test_engine_entry_slots_and_out(cuda, dtype, q_rank):
+    """The engine path (examples/ops.py:19-31): store each sequence's new token at
+    ``slots`` (negative skips), lens is the post-store length, caller-owned out."""
+    lens, h, d, page = [30, 64, 1], 4, 128, 16
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=9, device=cuda)
+    kn, vn = (torch.randn(len(lens), h, d).to(dtype).to(cuda) for _ in range(2))
+    qn = q[:, 0] if q_rank == 3 else q
+    pos = torch.tensor(lens)
+    slots = bt.cpu()[torch.arange(3), pos // page].long() * page + pos % page
+    slots[2] = -1  # sequence 2 stores nothing and attends its 1 cached key
+    post = torch.tensor([31, 65, 1], dtype=torch.int32, device=cuda)
+    out = torch.empty_like(qn)
+    mod = K.module()
+    kk, vv = (kn, vn) if q_rank == 3 else (kn[:, None], vn[:, None])
+    got = mod.decode(K.runtime(), qn, kc, vc, kk, vv, slots.to(cuda), post, bt, None, out)
+    assert got is out
+    ks2 = [torch.cat([ks[0], kn[None, 0:1]], 1), torch.cat([ks[1], kn[None, 1:2]], 1), ks[2]]
+    vs2 = [torch.cat([vs[0], vn[None, 0:1]], 1), torch.cat([vs[1], vn[None, 1:2]], 1), vs[2]]
+    ref = reference(q, ks2, vs2, d ** -0.5)
+    assert_close(out.view(ref.shape), ref, dtype, paged=True)
+    # declines: slots without k/v, a wrong-dtype out
+    assert mod.decode(K.runtime(), qn, kc, vc, None, None, slots.to(cuda), post, bt, None, None) is None
+    assert mod.decode(K.runtime(), qn, kc, vc, kk, vv, slots.to(cuda), post, bt, None,
+                      out.float() if dtype == torch.bfloat16 else out.bfloat16()) is None
+
+
+def test_host_checks_off_never_faults(cuda):
+    """Without the host read, out-of-range slots are not stored and lengths past the
+    table are clamped to its capacity: no fault, finite output."""
+    old = K.set_host_checks(False)
+    try:
+        h, d, page = 2, 64, 16
+        kc = torch.zeros(4, h, page, d, device=cuda)
+        vc = torch.zeros_like(kc)
+        key = torch.randn(3, h, d, device=cuda)
+        reshape_and_cache(key, key, kc, vc, torch.tensor([0, 10**6, -5], device=cuda))
+        kflat = kc[0].reshape(h, -1)
+        assert torch.equal(kflat[:, ::page], key[0])  # K word (d, t=0) sits at d*P
+        assert torch.equal(vc[0, :, 0], key[0])
+        assert int((kc != 0).sum()) == h * d and int((vc != 0).sum()) == h * d
+        q = torch.randn(2, 1, h, d, device=cuda)
+        bt = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32, device=cuda)
+        out = flash_attn_with_kvcache(q, kc, vc, cache_seqlens=torch.tensor([1000, 5], dtype=torch.int32,
+                                                                            device=cuda), page_table=bt)
+        assert torch.isfinite(out).all()
+    finally:
+        K.set_host_checks(old)
