@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecodeParams p) {
   constexpr int G = kWave / LPR;    // V rows per wave load
   constexpr int UNROLL = 16;
   static_assert(W % UNROLL == 0 && kUnit % G == 0, "tile shape");
-  __shared__ float p_lds[4][kTile];
+  __shared__ __attribute__((aligned(16))) float p_lds[4][kTile];
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int64_t pair = blockIdx.x;
@@ -107,15 +107,19 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecodeParams p) {
             k4[i] = *reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page);
 #pragma unroll
           for (int i = 0; i < UNROLL; ++i) {
-            const bf16x2 qv = __builtin_bit_cast(bf16x2, qw[w0 + i]);
-            a0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, k4[i].x), qv, a0, false);
-            a1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, k4[i].y), qv, a1, false);
-            a2 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, k4[i].z), qv, a2, false);
-            a3 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, k4[i].w), qv, a3, false);
+            const bf16x2 qv = as_bf16x2(qw[w0 + i]);
+            a0 = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(k4[i].x), qv, a0, false);
+            a1 = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(k4[i].y), qv, a1, false);
+            a2 = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(k4[i].z), qv, a2, false);
+            a3 = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(k4[i].w), qv, a3, false);
           }
         }
       } else {
+        // Four partial sums per key (words w mod 4): 32-term chains instead of one
+        // 128-term chain keep the fp32 logits well inside the 1e-6 decode gate.
         const float* qf = reinterpret_cast<const float*>(p.q) + seq * p.q_stride + h * E;
+        float c0[4] = {0.f, 0.f, 0.f, 0.f}, c1[4] = {0.f, 0.f, 0.f, 0.f};
+        float c2[4] = {0.f, 0.f, 0.f, 0.f}, c3[4] = {0.f, 0.f, 0.f, 0.f};
         for (int w0 = 0; w0 < W; w0 += UNROLL) {
           u32x4 k4[UNROLL];
 #pragma unroll
@@ -124,28 +128,36 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecodeParams p) {
 #pragma unroll
           for (int i = 0; i < UNROLL; ++i) {
             const float qv = qf[w0 + i];
-            a0 = fmaf(__uint_as_float(k4[i].x), qv, a0);
-            a1 = fmaf(__uint_as_float(k4[i].y), qv, a1);
-            a2 = fmaf(__uint_as_float(k4[i].z), qv, a2);
-            a3 = fmaf(__uint_as_float(k4[i].w), qv, a3);
+            c0[i & 3] = fmaf(__uint_as_float(k4[i].x), qv, c0[i & 3]);
+            c1[i & 3] = fmaf(__uint_as_float(k4[i].y), qv, c1[i & 3]);
+            c2[i & 3] = fmaf(__uint_as_float(k4[i].z), qv, c2[i & 3]);
+            c3[i & 3] = fmaf(__uint_as_float(k4[i].w), qv, c3[i & 3]);
           }
         }
+        a0 = (c0[0] + c0[1]) + (c0[2] + c0[3]);
+        a1 = (c1[0] + c1[1]) + (c1[2] + c1[3]);
+        a2 = (c2[0] + c2[1]) + (c2[2] + c2[3]);
+        a3 = (c3[0] + c3[1]) + (c3[2] + c3[3]);
       }
     }
+    // Raw logits (masked keys -inf); the scale is folded into the exponent below.
     const bool ok = kbu >= 0;
-    s[0] = (ok && key0 + 0 < len) ? a0 * p.c : -INFINITY;
-    s[1] = (ok && key0 + 1 < len) ? a1 * p.c : -INFINITY;
-    s[2] = (ok && key0 + 2 < len) ? a2 * p.c : -INFINITY;
-    s[3] = (ok && key0 + 3 < len) ? a3 * p.c : -INFINITY;
+    s[0] = (ok && key0 + 0 < len) ? a0 : -INFINITY;
+    s[1] = (ok && key0 + 1 < len) ? a1 : -INFINITY;
+    s[2] = (ok && key0 + 2 < len) ? a2 : -INFINITY;
+    s[3] = (ok && key0 + 3 < len) ? a3 : -INFINITY;
   }
 
-  // ---- softmax over the tile: p = 2^(logit*c - m), m the tile max.
-  float m = wave_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-  const float mu = m == -INFINITY ? 0.f : m;  // a tile with no readable key
+  // ---- softmax over the tile: m = max(logit)*c in scaled log2 units and
+  // p = 2^(logit*c - m), one rounding inside the exponent (the reference's
+  // fma(logit, c, -m), flash_vec.mojo:255-259; paged_attn.mojo:643-676).
+  const float mraw = wave_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+  const float m = mraw * p.c;
+  const float mu = mraw == -INFINITY ? 0.f : m;  // a tile with no readable key
   float pr[4], lsum = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    pr[j] = __builtin_amdgcn_exp2f(s[j] - mu);
+    pr[j] = __builtin_amdgcn_exp2f(fmaf(s[j], p.c, -mu));
     lsum += pr[j];
   }
   lsum = wave_sum(lsum);

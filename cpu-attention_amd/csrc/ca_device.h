@@ -19,6 +19,11 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 constexpr float kLog2e = 1.4426950408889634f;  // the reference's LOG2E (isa.mojo:58-62)
 constexpr int kWave = 64;
 
+// A 32-bit word as a bf16 pair.  Taking the word by value matters: hipcc (ROCm 7.2)
+// folds __builtin_bit_cast applied directly to an ext_vector element expression
+// (v.y, v.z, ...) onto element 0.
+__device__ __forceinline__ bf16x2 as_bf16x2(uint32_t w) { return __builtin_bit_cast(bf16x2, w); }
+
 // bf16 held as the high half of an fp32: widening is exact.
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

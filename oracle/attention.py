@@ -24,7 +24,7 @@ def attention(q, k, v, scale, causal=False):
     if causal:
         masked = np.arange(sk)[None, :] > np.arange(sq)[:, None] + sk - sq
         w = np.where(masked, -np.inf, w)
-    m = w.max(axis=-1, keepdims=True)
+    m = w.max(axis=-1, keepdims=True, initial=-np.inf)  # no keys at all: an empty row
     empty = ~np.isfinite(m)
     e = np.exp(w - np.where(empty, 0.0, m))
     s = e.sum(axis=-1, keepdims=True)

@@ -76,6 +76,8 @@ def test_attention_closed_forms():
     np.testing.assert_allclose(attention(q6, k, v, 0.5, True)[:, -1], attention(q6, k, v, 0.5)[:, -1])
     # row 0 of an sq = sk causal call sees only key 0
     np.testing.assert_allclose(attention(q6, k[:, :6], v[:, :6], 0.5, True)[:, 0], v[:, 0])
+    # no keys at all (a zero-length cache): the row is 0
+    assert np.all(attention(q, k[:, :0], v[:, :0], 0.5) == 0)
     # non-causal attention ignores the order of the keys
     perm = rng.permutation(9)
     np.testing.assert_allclose(attention(q, k, v, 0.4), attention(q, k[:, perm], v[:, perm], 0.4),
