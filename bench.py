@@ -180,7 +180,7 @@ def main():
         "us_per_call_median": round(float(np.median(ms)) * 1e3, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs_kernel, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs_kernel / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_partial_kernel<128,bf16> + decode_combine_kernel (one call)",
+                     "kernel": "decode_tiles_kernel<128,bf16> + decode_tiles_combine_kernel<128,bf16> (one call)",
                      "algorithmic_bytes": w["bytes"]},
     }
     del w

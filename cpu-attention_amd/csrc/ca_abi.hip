@@ -60,15 +60,19 @@ extern "C" int ca_store(const ca_store_args* a, void* stream) {
   return store_launch(p, (int)words, static_cast<hipStream_t>(stream));
 }
 
+// Workspace layout: fp32 partial accumulators [slots, E], then (max, sum) pairs
+// [slots, 2], one slot per (row, 256-key tile of the page table's capacity).
+static int64_t decode_acc_bytes(int64_t slots, int64_t head_dim) {
+  return ((slots * head_dim * 4 + 255) / 256) * 256;
+}
+
 extern "C" int64_t ca_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads,
                                              int64_t head_dim, int64_t page_size,
                                              int64_t page_table_width) {
   if (num_seqs < 0 || num_heads < 0 || page_size <= 0 || page_table_width < 0) return -1;
-  const int64_t tiles = decode_tiles(page_table_width, page_size);
-  // partial accumulators [N*H, tiles, E] then (max, sum) pairs [N*H, tiles, 2]
-  const int64_t acc = num_seqs * num_heads * tiles * head_dim * 4;
-  const int64_t ml = num_seqs * num_heads * tiles * 2 * 4;
-  return ((acc + 255) / 256) * 256 + ml;
+  const int64_t slots = decode_workspace_slots(num_seqs * num_heads,
+                                               decode_tiles(page_table_width, page_size));
+  return decode_acc_bytes(slots, head_dim) + slots * 2 * 4;
 }
 
 extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
@@ -129,8 +133,8 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
   p.nseqs = a->num_seqs;
   p.c = a->scale * kLog2e;
   p.tiles = (int)decode_tiles(a->page_table_width, a->page_size);
-  const int64_t acc_bytes =
-      ((a->num_seqs * a->num_heads * p.tiles * a->head_dim * 4 + 255) / 256) * 256;
+  p.slots = decode_workspace_slots(a->num_seqs * a->num_heads, p.tiles);
+  const int64_t acc_bytes = decode_acc_bytes(p.slots, a->head_dim);
   p.part_acc = static_cast<float*>(a->workspace);
   p.part_ml = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + acc_bytes);
   p.out = a->out;

@@ -1,5 +1,4 @@
-// Paged decode, split-K: one wave scores one 256-key tile of one (sequence, head)
-// and leaves a partial (max, sum, P@V) that a combine pass merges.
+// Paged decode on CDNA4: split-K over 256-key tiles plus a combine pass.
 //
 // Follows the reference's decode (cpu_attention/_mojo/src/paged_attn.mojo:714-782):
 // logits q.k, base-2 online softmax with c = scale*log2(e) and the running max in
@@ -8,22 +7,33 @@
 // never read (0 * NaN would poison the row, :686-687), nor are page-table entries
 // past the last page in use.
 //
+// Work split.  One wave per 256-key tile of one row (sequence, head): grid.x walks
+// the rows, grid.y the tile groups (4 tiles per 256-thread block) up to the page
+// table's capacity, so every row's first tiles are dispatched first and tiles
+// past a row's length exit at once.  A row that fits one tile is written by that
+// tile; otherwise each tile leaves a partial (max, sum, P.V) and the combine
+// kernel merges them.  The host needs no lengths and nothing synchronises.  (A
+// stream-K split into equal slices per resident wave was measured slower: 347 us
+// against 189 us on the bench's batch.)
+//
 // Layout use (the reference's PageLayout, :58-130): a 16-key unit never straddles a
-// page (P % 16 == 0), so a tile is 16 units, each one contiguous run inside one
+// page (P % 16 == 0), so a tile is up to 16 units, each one contiguous run inside one
 // (block, head):
 //   Q.K  lane l owns keys 4l..4l+3 of the tile; one 16-byte load per K word row
 //        (w*P + t .. t+3) gives those 4 keys' word w, so the dot product needs no
 //        cross-lane reduction.  bf16 words are dim pairs: v_dot2_f32_bf16 with the
 //        matching q pair (exact products, fp32 accumulation).
 //   P.V  lane groups of E/8 (bf16) or E/4 (fp32) lanes read whole V rows with
-//        16-byte loads, G rows per wave instruction; p comes from LDS.
+//        16-byte loads; each wave instruction reads rows of G different units
+//        (pages), p comes from LDS.
+// K and V are read with non-temporal loads: each byte is used once.
 #include "ca_device.h"
 #include "ca_internal.h"
 
 namespace ca {
 
-constexpr int kTile = 256;  // keys per wave tile
-constexpr int kUnit = 16;   // keys per unit (one page run)
+constexpr int kTile = 256;    // keys per tile
+constexpr int kUnit = 16;     // keys per unit (one page run)
 
 // out[idx .. idx+N) = v * inv in the output dtype (bf16: round to nearest even).
 template <int N, bool BF>
@@ -43,59 +53,70 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, const float* v
   }
 }
 
-__device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
-  const int lo = __builtin_amdgcn_readlane((int)(x & 0xffffffff), lane);
-  const int hi = __builtin_amdgcn_readlane((int)(x >> 32), lane);
-  return (int64_t)(uint32_t)lo | ((int64_t)hi << 32);
+__device__ __forceinline__ int64_t row_len(const DecodeParams& p, int64_t seq) {
+  const int64_t cap = p.pt_width * p.page;
+  const int64_t len = (int64_t)p.lens[seq] + p.len_add;
+  return len < 0 ? 0 : (len < cap ? len : cap);
 }
 
 template <int E, bool BF>
-__global__ __launch_bounds__(256) void decode_partial_kernel(DecodeParams p) {
-  constexpr int ES = BF ? 2 : 4;    // element bytes
-  constexpr int W = E * ES / 4;     // K words per key (per head)
-  constexpr int DPL = 16 / ES;      // V elements per 16-byte load
-  constexpr int LPR = E / DPL;      // lanes per V row
-  constexpr int G = kWave / LPR;    // V rows per wave load
-  constexpr int UNROLL = 16;
+struct DecodeShape {
+  static constexpr int ES = BF ? 2 : 4;    // element bytes
+  static constexpr int W = E * ES / 4;     // K words per key (per head)
+  static constexpr int DPL = 16 / ES;      // V elements per 16-byte load
+  static constexpr int LPR = E / DPL;      // lanes per V row
+  static constexpr int G = kWave / LPR;    // V rows per wave load
+  static constexpr int UNROLL = 16;
   static_assert(W % UNROLL == 0 && kUnit % G == 0, "tile shape");
-  __shared__ __attribute__((aligned(16))) float p_lds[4][kTile];
+};
 
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int64_t pair = blockIdx.x;
-  const int64_t seq = pair / p.heads, h = pair - seq * p.heads;
-  const int tile = blockIdx.y * 4 + wv;
-  const int64_t cap = p.pt_width * p.page;
-  int64_t len = (int64_t)p.lens[seq] + p.len_add;
-  len = len < cap ? len : cap;
-  const int64_t t0 = (int64_t)tile * kTile;
-  if (len <= 0 || t0 >= len) return;
-  const int ntok = (int)min<int64_t>(kTile, len - t0);
+// Online-softmax state of one wave for one row: m (scaled log2 units, uniform),
+// l (per-lane partial sum), acc (per-lane partial P.V of dims dl*DPL.., summed over
+// the lane groups at the end).
+template <int E, bool BF>
+struct RowState {
+  float m, l;
+  float acc[DecodeShape<E, BF>::DPL];
+  __device__ void init() {
+    m = -INFINITY;
+    l = 0.f;
+#pragma unroll
+    for (int i = 0; i < DecodeShape<E, BF>::DPL; ++i) acc[i] = 0.f;
+  }
+};
+
+// Keys [t0, t0 + ntok) of row (seq, h): 0 < ntok <= 256, t0 % 16 == 0, t0 + ntok <= len.
+// Folds them into st.  p_lds is this wave's 256-float scratch.
+template <int E, bool BF>
+__device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, int64_t h,
+                                            int64_t t0, int ntok, float* p_lds,
+                                            RowState<E, BF>& st) {
+  using D = DecodeShape<E, BF>;
+  constexpr int W = D::W, DPL = D::DPL, LPR = D::LPR, G = D::G, ES = D::ES, UNROLL = D::UNROLL;
+  const int lane = threadIdx.x & 63;
 
   // Unit table: lane u < 16 resolves unit u's page once (word index of its K run,
-  // element index of its V rows); -1 marks a unit past the length or a page-table
+  // element index of its V rows); -1 marks a unit past the tile or a page-table
   // entry that names no block.
   int64_t kb = -1, vb = -1;
-  if (lane < kTile / kUnit) {
+  if (lane < kTile / kUnit && kUnit * lane < ntok) {
     const int64_t tu = t0 + kUnit * lane;
-    if (tu < len) {
-      const int64_t pi = tu / p.page, off = tu - pi * p.page;
-      const int64_t blk = p.page_table[seq * p.pt_width + pi];
-      if (blk >= 0 && blk < p.nblocks) {
-        const int64_t base = (blk * p.heads + h) * p.page;
-        kb = base * W + off;
-        vb = (base + off) * E;
-      }
+    const int64_t pi = tu / p.page, off = tu - pi * p.page;
+    const int64_t blk = p.page_table[seq * p.pt_width + pi];
+    if (blk >= 0 && blk < p.nblocks) {
+      const int64_t base = (blk * p.heads + h) * p.page;
+      kb = base * W + off;
+      vb = (base + off) * E;
     }
   }
 
   // ---- Q.K: keys 4*lane .. 4*lane+3 of the tile.
   float s[4];
   {
-    const int u = lane >> 2;
-    const int64_t kbu = __shfl(kb, u);
-    const int64_t key0 = t0 + 4 * lane;
+    const int64_t kbu = __shfl(kb, lane >> 2);
+    const int key0 = 4 * lane;
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    if (kbu >= 0 && key0 < len) {
+    if (kbu >= 0 && key0 < ntok) {
       const uint32_t* kp = p.kc + kbu + 4 * (lane & 3);
       if constexpr (BF) {
         const uint32_t* qw = reinterpret_cast<const uint32_t*>(
@@ -104,7 +125,8 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecodeParams p) {
           u32x4 k4[UNROLL];
 #pragma unroll
           for (int i = 0; i < UNROLL; ++i)
-            k4[i] = *reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page);
+            k4[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page));
 #pragma unroll
           for (int i = 0; i < UNROLL; ++i) {
             const bf16x2 qv = as_bf16x2(qw[w0 + i]);
@@ -124,7 +146,8 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecodeParams p) {
           u32x4 k4[UNROLL];
 #pragma unroll
           for (int i = 0; i < UNROLL; ++i)
-            k4[i] = *reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page);
+            k4[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page));
 #pragma unroll
           for (int i = 0; i < UNROLL; ++i) {
             const float qv = qf[w0 + i];
@@ -142,154 +165,185 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecodeParams p) {
     }
     // Raw logits (masked keys -inf); the scale is folded into the exponent below.
     const bool ok = kbu >= 0;
-    s[0] = (ok && key0 + 0 < len) ? a0 : -INFINITY;
-    s[1] = (ok && key0 + 1 < len) ? a1 : -INFINITY;
-    s[2] = (ok && key0 + 2 < len) ? a2 : -INFINITY;
-    s[3] = (ok && key0 + 3 < len) ? a3 : -INFINITY;
+    s[0] = (ok && key0 + 0 < ntok) ? a0 : -INFINITY;
+    s[1] = (ok && key0 + 1 < ntok) ? a1 : -INFINITY;
+    s[2] = (ok && key0 + 2 < ntok) ? a2 : -INFINITY;
+    s[3] = (ok && key0 + 3 < ntok) ? a3 : -INFINITY;
   }
 
-  // ---- softmax over the tile: m = max(logit)*c in scaled log2 units and
-  // p = 2^(logit*c - m), one rounding inside the exponent (the reference's
-  // fma(logit, c, -m), flash_vec.mojo:255-259; paged_attn.mojo:643-676).
+  // ---- online softmax: tile max in scaled log2 units, alpha = 2^(m_old - m_new)
+  // (0 on the first tile), p = 2^(logit*c - m): one rounding inside the exponent
+  // (the reference's _rescale / _exp_row, paged_attn.mojo:271-277, 643-676).
   const float mraw = wave_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-  const float m = mraw * p.c;
-  const float mu = mraw == -INFINITY ? 0.f : m;  // a tile with no readable key
-  float pr[4], lsum = 0.f;
+  const float m_new = fmaxf(st.m, mraw * p.c);
+  const float mu = m_new == -INFINITY ? 0.f : m_new;  // nothing readable yet
+  const float alpha = __builtin_amdgcn_exp2f(st.m - mu);
+  st.m = m_new;
+  float pr[4];
+  float ls = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     pr[j] = __builtin_amdgcn_exp2f(fmaf(s[j], p.c, -mu));
-    lsum += pr[j];
+    ls += pr[j];
   }
-  lsum = wave_sum(lsum);
-  *reinterpret_cast<f32x4*>(&p_lds[wv][4 * lane]) = f32x4{pr[0], pr[1], pr[2], pr[3]};
+  st.l = fmaf(st.l, alpha, ls);
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) st.acc[i] *= alpha;
+  wave_lds_sync();  // the previous tile's P.V reads are done
+  *reinterpret_cast<f32x4*>(&p_lds[4 * lane]) = f32x4{pr[0], pr[1], pr[2], pr[3]};
   wave_lds_sync();
 
-  // ---- P.V: lane (g, dl) takes dims dl*DPL.. of keys g, g+G, ... of each unit.
+  // ---- P.V: lane group g (of G) takes units g*UPG .. g*UPG+UPG-1 of the tile,
+  // lane dl of the group dims dl*DPL..  Load j of a lane reads row j / UPG of unit
+  // g*UPG + j % UPG, so one wave instruction spans G units and a batch of 16 loads
+  // spans every unit of the group: the reads fan out over many pages at once,
+  // which streams far better than walking one page row by row.
+  constexpr int UPG = kTile / kUnit / G;   // units per group
+  constexpr int R = kUnit * UPG;           // rows per lane
+  constexpr int B = R < 16 ? R : 16;       // loads in flight
   const int g = lane / LPR, dl = lane - g * LPR;
-  float acc[DPL];
+  int64_t vbu[UPG];
 #pragma unroll
-  for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+  for (int k = 0; k < UPG; ++k) vbu[k] = __shfl(vb, g * UPG + k);
   const char* vbase = reinterpret_cast<const char*>(p.vc) + dl * 16;
-  const int nunits = (ntok + kUnit - 1) / kUnit;
-  constexpr int LPU = kUnit / G;                  // V loads per unit per lane
-  constexpr int UG = LPU >= 16 ? 1 : 16 / LPU;    // units per batch: 16 loads in flight
-  for (int u0 = 0; u0 < nunits; u0 += UG) {
-    u32x4 v4[UG][LPU];
-    bool ok[UG][LPU];
+  const int t_first = kUnit * g * UPG;     // this group's first token in the tile
 #pragma unroll
-    for (int uu = 0; uu < UG; ++uu) {
-      const int u = u0 + uu;  // < 16: UG divides the 16 units of a tile
-      const int64_t vbu = readlane64(vb, u);
+  for (int b0 = 0; b0 < R; b0 += B) {
+    if (t_first + b0 / UPG >= ntok) break;  // nothing left for this group
+    u32x4 v4[B];
+    bool ok[B];
 #pragma unroll
-      for (int jj = 0; jj < LPU; ++jj) {
-        const int x = jj * G + g;
-        ok[uu][jj] = vbu >= 0 && kUnit * u + x < ntok;
-        if (ok[uu][jj])
-          v4[uu][jj] = *reinterpret_cast<const u32x4*>(vbase + (vbu + (int64_t)x * E) * ES);
-      }
+    for (int i = 0; i < B; ++i) {
+      const int j = b0 + i, k = j % UPG, x = j / UPG;
+      ok[i] = vbu[k] >= 0 && t_first + kUnit * k + x < ntok;
+      if (ok[i])
+        v4[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(vbase + (vbu[k] + (int64_t)x * E) * ES));
     }
 #pragma unroll
-    for (int uu = 0; uu < UG; ++uu) {
-#pragma unroll
-      for (int jj = 0; jj < LPU; ++jj) {
-        if (ok[uu][jj]) {
-          const float pj = p_lds[wv][kUnit * (u0 + uu) + jj * G + g];
-          const u32x4 v = v4[uu][jj];
-          if constexpr (BF) {
-            acc[0] = fmaf(pj, bf16_lo(v.x), acc[0]);
-            acc[1] = fmaf(pj, bf16_hi(v.x), acc[1]);
-            acc[2] = fmaf(pj, bf16_lo(v.y), acc[2]);
-            acc[3] = fmaf(pj, bf16_hi(v.y), acc[3]);
-            acc[4] = fmaf(pj, bf16_lo(v.z), acc[4]);
-            acc[5] = fmaf(pj, bf16_hi(v.z), acc[5]);
-            acc[6] = fmaf(pj, bf16_lo(v.w), acc[6]);
-            acc[7] = fmaf(pj, bf16_hi(v.w), acc[7]);
-          } else {
-            acc[0] = fmaf(pj, __uint_as_float(v.x), acc[0]);
-            acc[1] = fmaf(pj, __uint_as_float(v.y), acc[1]);
-            acc[2] = fmaf(pj, __uint_as_float(v.z), acc[2]);
-            acc[3] = fmaf(pj, __uint_as_float(v.w), acc[3]);
-          }
+    for (int i = 0; i < B; ++i) {
+      const int j = b0 + i, k = j % UPG, x = j / UPG;
+      if (ok[i]) {
+        const float pj = p_lds[t_first + kUnit * k + x];
+        const u32x4 v = v4[i];
+        if constexpr (BF) {
+          st.acc[0] = fmaf(pj, bf16_lo(v.x), st.acc[0]);
+          st.acc[1] = fmaf(pj, bf16_hi(v.x), st.acc[1]);
+          st.acc[2] = fmaf(pj, bf16_lo(v.y), st.acc[2]);
+          st.acc[3] = fmaf(pj, bf16_hi(v.y), st.acc[3]);
+          st.acc[4] = fmaf(pj, bf16_lo(v.z), st.acc[4]);
+          st.acc[5] = fmaf(pj, bf16_hi(v.z), st.acc[5]);
+          st.acc[6] = fmaf(pj, bf16_lo(v.w), st.acc[6]);
+          st.acc[7] = fmaf(pj, bf16_hi(v.w), st.acc[7]);
+        } else {
+          st.acc[0] = fmaf(pj, __uint_as_float(v.x), st.acc[0]);
+          st.acc[1] = fmaf(pj, __uint_as_float(v.y), st.acc[1]);
+          st.acc[2] = fmaf(pj, __uint_as_float(v.z), st.acc[2]);
+          st.acc[3] = fmaf(pj, __uint_as_float(v.w), st.acc[3]);
         }
-      }
-    }
-  }
-#pragma unroll
-  for (int o = LPR; o < kWave; o <<= 1)
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) acc[i] += __shfl_xor(acc[i], o);
-
-  if (g == 0) {
-    if (len <= kTile) {
-      // The only tile of this row: write the output here (the combine skips it).
-      store_out<DPL, BF>(p.out, pair * E + dl * DPL, acc, lsum > 0.f ? 1.f / lsum : 0.f);
-    } else {
-      float* pa = p.part_acc + (pair * p.tiles + tile) * E + dl * DPL;
-#pragma unroll
-      for (int i = 0; i < DPL; i += 4)
-        *reinterpret_cast<f32x4*>(pa + i) = f32x4{acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
-      if (lane == 0) {
-        p.part_ml[(pair * p.tiles + tile) * 2 + 0] = m;
-        p.part_ml[(pair * p.tiles + tile) * 2 + 1] = lsum;
       }
     }
   }
 }
 
-// One wave per (sequence, head): merge the tiles' partials into the output.
+// Ends a piece of a row: reduce the lane partials and write either the output
+// (the piece was the whole row) or a partial into workspace slot `slot`.
 template <int E, bool BF>
-__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
-  constexpr int DPC = E >= 64 ? E / 64 : 1;  // dims per lane
+__device__ __forceinline__ void finish_piece(const DecodeParams& p, RowState<E, BF>& st,
+                                             int64_t row, bool whole, int64_t slot) {
+  using D = DecodeShape<E, BF>;
+  constexpr int DPL = D::DPL, LPR = D::LPR;
+  const int lane = threadIdx.x & 63;
+  const float l = wave_sum(st.l);
+#pragma unroll
+  for (int o = LPR; o < kWave; o <<= 1)
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) st.acc[i] += __shfl_xor(st.acc[i], o);
+  if (lane < LPR) {
+    if (whole) {
+      store_out<DPL, BF>(p.out, row * E + lane * DPL, st.acc, l > 0.f ? 1.f / l : 0.f);
+    } else {
+      float* pa = p.part_acc + slot * E + lane * DPL;
+#pragma unroll
+      for (int i = 0; i < DPL; i += 4)
+        *reinterpret_cast<f32x4*>(pa + i) = f32x4{st.acc[i], st.acc[i + 1], st.acc[i + 2], st.acc[i + 3]};
+      if (lane == 0) {
+        p.part_ml[2 * slot] = st.m;
+        p.part_ml[2 * slot + 1] = l;
+      }
+    }
+  }
+}
+
+// One wave per 256-key tile of each row.
+template <int E, bool BF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+void decode_tiles_kernel(DecodeParams p) {
+  __shared__ __attribute__((aligned(16))) float p_lds[4][kTile];
+  const int wv = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  const int64_t s = row / p.heads, h = row - s * p.heads;
+  const int64_t tile = (int64_t)blockIdx.y * 4 + wv;
+  const int64_t len = row_len(p, s);
+  const int64_t t0 = tile * kTile;
+  if (t0 >= len) return;
+  RowState<E, BF> st;
+  st.init();
+  decode_tile<E, BF>(p, s, h, t0, (int)min<int64_t>(kTile, len - t0), p_lds[wv], st);
+  finish_piece<E, BF>(p, st, row, len <= kTile, row * p.tiles + tile);
+}
+
+template <int E, bool BF>
+__global__ __launch_bounds__(256) void decode_tiles_combine_kernel(DecodeParams p) {
+  constexpr int DPC = E >= 64 ? E / 64 : 1;
   constexpr int ACTIVE = E / DPC;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int64_t pair = (int64_t)blockIdx.x * 4 + wv;
-  if (pair >= p.nseqs * p.heads) return;
-  const int64_t seq = pair / p.heads;
-  const int64_t cap = p.pt_width * p.page;
-  int64_t len = (int64_t)p.lens[seq] + p.len_add;
-  len = len < cap ? len : cap;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.nseqs * p.heads) return;
+  const int64_t len = row_len(p, row / p.heads);
+  if (len > 0 && len <= kTile) return;  // written by the tile itself
   float acc[DPC];
 #pragma unroll
   for (int i = 0; i < DPC; ++i) acc[i] = 0.f;
-  if (len > 0 && len <= kTile) return;  // written by the tile itself
   float inv = 0.f;
   if (len > 0) {
-    const int nt = (int)((len + kTile - 1) / kTile);
-    const float* ml = p.part_ml + pair * p.tiles * 2;
+    const int64_t nt = cdiv(len, kTile);
+    const float* ml = p.part_ml + row * p.tiles * 2;
     float mx = -INFINITY;
-    for (int t = lane; t < nt; t += kWave) mx = fmaxf(mx, ml[2 * t]);
+    for (int64_t t = lane; t < nt; t += kWave) mx = fmaxf(mx, ml[2 * t]);
     mx = wave_max(mx);
     if (mx != -INFINITY) {
       float l = 0.f;
-      const float* pa = p.part_acc + pair * p.tiles * E + lane * DPC;
-      for (int t = 0; t < nt; ++t) {
+      const float* pa = p.part_acc + row * p.tiles * E + lane * DPC;
+      for (int64_t t = 0; t < nt; ++t) {
         const float wgt = __builtin_amdgcn_exp2f(ml[2 * t] - mx);
         l = fmaf(wgt, ml[2 * t + 1], l);
         if (lane < ACTIVE) {
 #pragma unroll
-          for (int i = 0; i < DPC; ++i) acc[i] = fmaf(wgt, pa[(int64_t)t * E + i], acc[i]);
+          for (int i = 0; i < DPC; ++i) acc[i] = fmaf(wgt, pa[t * E + i], acc[i]);
         }
       }
       inv = l > 0.f ? 1.f / l : 0.f;
     }
   }
-  if (lane < ACTIVE) store_out<DPC, BF>(p.out, pair * E + lane * DPC, acc, inv);
+  if (lane < ACTIVE) store_out<DPC, BF>(p.out, row * E + lane * DPC, acc, inv);
 }
 
 int64_t decode_tiles(int64_t pt_width, int64_t page) { return cdiv(pt_width * page, kTile); }
 
+// Partial slots the workspace must hold: one per (row, tile).
+int64_t decode_workspace_slots(int64_t rows, int64_t tiles) { return rows * tiles; }
+
 template <int E, bool BF>
 static int decode_launch_t(const DecodeParams& p, hipStream_t stream) {
-  const int64_t pairs = p.nseqs * p.heads;
+  const int64_t rows = p.nseqs * p.heads;
   const int64_t gy = cdiv(p.tiles, 4);
-  if (pairs > 0x7fffffff || gy > 65535) return CA_DECLINED;
-  // grid.x = (sequence, head), grid.y = tile group: every row's first tiles are
-  // dispatched first, the (mostly empty) tail tiles of short rows last.
-  hipLaunchKernelGGL((decode_partial_kernel<E, BF>), dim3((unsigned)pairs, (unsigned)gy),
-                     dim3(256), 0, stream, p);
+  if (rows > 0x7fffffff || gy > 65535 || rows * p.tiles > p.slots) return CA_DECLINED;
+  hipLaunchKernelGGL((decode_tiles_kernel<E, BF>), dim3((unsigned)rows, (unsigned)gy), dim3(256), 0,
+                     stream, p);
   int st = ca_launch_status();
   if (st != CA_OK) return st;
-  hipLaunchKernelGGL((decode_combine_kernel<E, BF>), dim3((unsigned)cdiv(pairs, 4)), dim3(256),
+  hipLaunchKernelGGL((decode_tiles_combine_kernel<E, BF>), dim3((unsigned)cdiv(rows, 4)), dim3(256),
                      0, stream, p);
   return ca_launch_status();
 }

@@ -32,9 +32,10 @@ struct DecodeParams {
   int64_t pt_width;
   int64_t heads, page, nblocks, nseqs;
   float c;                // softmax scale * log2(e)
-  int tiles;              // key tiles per (sequence, head) slot in the workspace
-  float* part_acc;        // [N*H, tiles, E]
-  float* part_ml;         // [N*H, tiles, 2]: running max (scaled log2 units), sum
+  int tiles;              // 256-key tiles per row at the page table's capacity
+  int64_t slots;          // partial slots the workspace holds
+  float* part_acc;        // [slots, E]
+  float* part_ml;         // [slots, 2]: running max (scaled log2 units), sum
   void* out;              // [N, H, E] contiguous
 };
 
@@ -51,6 +52,7 @@ struct FlashParams {
 
 int store_launch(const StoreParams& p, int words, hipStream_t stream);
 int64_t decode_tiles(int64_t pt_width, int64_t page);
+int64_t decode_workspace_slots(int64_t rows, int64_t tiles);
 int decode_launch(const DecodeParams& p, int head_dim, int bf16, hipStream_t stream);
 int flash_launch(const FlashParams& p, int head_dim, int bf16, hipStream_t stream);
 

@@ -12,7 +12,7 @@ import torch
 
 from cpu_attention import _kernel as K
 from cpu_attention import flash_attn_with_kvcache, reshape_and_cache
-from helpers import (NAME, appended, assert_close, cache_words, layout, reference, row_words,
+from helpers import (NAME, appended, assert_close, attention, cache_words, layout, reference, row_words,
                      stage, values)
 
 pytestmark = pytest.mark.gpu
@@ -231,3 +231,36 @@ def test_host_checks_off_never_faults(cuda):
         assert torch.isfinite(out).all()
     finally:
         K.set_host_checks(old)
+
+
+@pytest.mark.parametrize("nseqs", [4095, 4100])
+def test_many_sequences(cuda, nseqs):
+    """Thousands of short rows, many of them empty: one wave per 256-key tile of
+    8190+ rows, single-tile rows written directly.  Every row checked."""
+    h, d, page = 2, 32, 16
+    rng = np.random.default_rng(nseqs)
+    lens = rng.integers(0, 300, size=nseqs)
+    lens[::97] = 0
+    width = -(-int(lens.max()) // page)
+    nb = nseqs * width
+    table = torch.from_numpy(rng.permutation(nb).astype(np.int32)).view(nseqs, width)
+    g = torch.Generator().manual_seed(nseqs)
+    kc = torch.full((nb, h, page, d), float("nan"), dtype=torch.bfloat16, device=cuda)
+    vc = torch.full_like(kc, float("nan"))
+    total = int(lens.sum())
+    key = torch.randn(total, h, d, generator=g).bfloat16()
+    value = torch.randn(total, h, d, generator=g).bfloat16()
+    slots = np.concatenate([layout.prompt_slots(0, int(m), table[i].numpy(), page)
+                            for i, m in enumerate(lens)])
+    reshape_and_cache(key.to(cuda), value.to(cuda), kc, vc, torch.from_numpy(slots).to(cuda))
+    q = torch.randn(nseqs, 1, h, d, generator=g).bfloat16()
+    out = flash_attn_with_kvcache(q.to(cuda), kc, vc, page_table=table.to(cuda),
+                                  cache_seqlens=torch.from_numpy(lens.astype(np.int32)).to(cuda))
+    starts = np.concatenate([[0], np.cumsum(lens)])
+    kv, vv, qv = values(key), values(value), values(q)
+    ref = np.zeros((nseqs, 1, h, d))
+    for i, m in enumerate(lens):
+        if m:
+            ref[i] = attention(qv[i:i + 1], kv[None, starts[i]:starts[i + 1]],
+                               vv[None, starts[i]:starts[i + 1]], d ** -0.5)[0]
+    assert_close(out, ref, torch.bfloat16, paged=True)
