@@ -7,7 +7,9 @@
 //
 // Block = 4 waves x 32 query rows.  Each wave keeps its Q rows in registers and
 // walks the key range in tiles staged through LDS (double-buffered; the next tile's
-// global loads are in flight while the current one is consumed):
+// buffer loads are in flight while the current one is consumed, one barrier per
+// tile).  The loop body is branch-free around the loads: a conditional prefetch
+// made the compiler wait for it before the first MFMA of every tile.
 //
 //   S^T = K Q^T   32x32 MFMA tiles with keys as rows and queries as columns, so a
 //                 lane ends up owning one query and 16 keys of each tile;
@@ -26,6 +28,18 @@
 namespace ca {
 
 constexpr int kBM = 128;  // query rows per block (4 waves x 32)
+
+// A raw buffer resource over [base, base + bytes): loads past `bytes` return 0.
+// The per-tile K/V loads rebase the resource at each tile, so their per-lane
+// offsets stay fixed across the loop (no address registers rewritten under
+// in-flight loads) and rows past the last key come back as zeros.
+// A tile that starts past the last key (the prefetch after the last tile) has a
+// negative byte count: it becomes an empty window, where every load reads zero
+// without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int64_t bytes) {
+  const int64_t n = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
 
 // Hardware dispatches workgroup i to XCD i % 8.  Remap so each XCD walks a
 // contiguous range of (batch*head, query block) work: one head's K/V stays in
@@ -89,8 +103,19 @@ __global__ __launch_bounds__(256, 2) void flash_bf16_kernel(FlashParams p) {
   const uint16_t* kg = reinterpret_cast<const uint16_t*>(p.k) + bw.b * p.ks[0] + bw.h * p.ks[2];
   const uint16_t* vg = reinterpret_cast<const uint16_t*>(p.v) + bw.b * p.vs[0] + bw.h * p.vs[2];
 
-  // Q rows of this wave as B operands: lane (query li, half hf) holds dims 16s+8hf..+7.
   const int64_t row = bw.q0 + 32 * wv + li;
+  const int64_t kend_blk = p.causal ? min<int64_t>(S, bw.q0 + kBM + diag) : S;
+  const int nkt = kend_blk > 0 ? (int)cdiv(kend_blk, BN) : 0;
+  if (nkt == 0) {  // every row of the block sees no key: exactly 0
+    if (row < L) {
+      uint16_t* og = reinterpret_cast<uint16_t*>(p.out) + ((bw.b * L + row) * p.heads + bw.h) * E;
+#pragma unroll
+      for (int d = 0; d < E / 2; d += 8) *reinterpret_cast<u32x4*>(og + (E / 2) * hf + d) = u32x4{0, 0, 0, 0};
+    }
+    return;
+  }
+
+  // Q rows of this wave as B operands: lane (query li, half hf) holds dims 16s+8hf..+7.
   bf16x8 qr[E / 16];
 #pragma unroll
   for (int s = 0; s < E / 16; ++s) {
@@ -99,33 +124,31 @@ __global__ __launch_bounds__(256, 2) void flash_bf16_kernel(FlashParams p) {
     qr[s] = __builtin_bit_cast(bf16x8, v);
   }
 
-  const int64_t kend_blk = p.causal ? min<int64_t>(S, bw.q0 + kBM + diag) : S;
-  const int nkt = kend_blk > 0 ? (int)cdiv(kend_blk, BN) : 0;
   const int64_t r0w = bw.q0 + 32 * wv;  // first row of this wave
   const int64_t kend_w = p.causal ? min<int64_t>(S, r0w + 32 + diag) : S;
 
-  // Global -> register staging of one K/V tile.
+  // Global -> register staging of one K/V tile through buffer loads: fixed per-lane
+  // byte offsets, the resource rebased at the tile; rows past S read as zeros.
   u32x4 kreg[C::KCH];
   u32x4 vreg[4];
+  int koff[C::KCH], voff[4];
+#pragma unroll
+  for (int i = 0; i < C::KCH; ++i) {
+    const int c = tid + 256 * i;
+    koff[i] = (int)(((c / (E / 8)) * p.ks[1] + 8 * (c % (E / 8))) * 2);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) voff[r] = (int)(((4 * (tid & 15) + r) * p.vs[1] + 8 * (tid >> 4)) * 2);
   auto load_tile = [&](int t) {
     const int64_t k0 = (int64_t)t * BN;
+    const int64_t kbytes = ((S - 1 - k0) * p.ks[1] + E) * 2, vbytes = ((S - 1 - k0) * p.vs[1] + E) * 2;
+    const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kg + k0 * p.ks[1], kbytes);
+    const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vg + k0 * p.vs[1], vbytes);
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int c = tid + 256 * i;
-      const int r = c / (E / 8), c8 = c % (E / 8);
-      u32x4 v = {0, 0, 0, 0};
-      if (k0 + r < S) v = *reinterpret_cast<const u32x4*>(kg + (k0 + r) * p.ks[1] + 8 * c8);
-      kreg[i] = v;
-    }
-    if (tid < C::VBLK) {
-      const int kgp = tid & 15, dc = tid >> 4;
+    for (int i = 0; i < C::KCH; ++i) kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0);
+    if (C::VBLK >= 256 || tid < C::VBLK) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t key = k0 + 4 * kgp + r;
-        u32x4 v = {0, 0, 0, 0};
-        if (key < S) v = *reinterpret_cast<const u32x4*>(vg + key * p.vs[1] + 8 * dc);
-        vreg[r] = v;
-      }
+      for (int r = 0; r < 4; ++r) vreg[r] = __builtin_amdgcn_raw_buffer_load_b128(vr, voff[r], 0, 0);
     }
   };
   auto store_tile = [&](int buf) {
@@ -136,7 +159,7 @@ __global__ __launch_bounds__(256, 2) void flash_bf16_kernel(FlashParams p) {
       const int r = c / (E / 8), c8 = c % (E / 8);
       *reinterpret_cast<u32x4*>(kb + r * KS + 8 * c8) = kreg[i];
     }
-    if (tid < C::VBLK) {
+    if (C::VBLK >= 256 || tid < C::VBLK) {
       const int kgp = tid & 15, dc = tid >> 4;
       uint16_t* vb = Vt + buf * C::LDS_V + (8 * dc) * VS + vt_pos(4 * kgp);
       const uint32_t w0[4] = {vreg[0].x, vreg[0].y, vreg[0].z, vreg[0].w};
@@ -167,7 +190,7 @@ __global__ __launch_bounds__(256, 2) void flash_bf16_kernel(FlashParams p) {
   __syncthreads();
   for (int t = 0; t < nkt; ++t) {
     const int buf = t & 1;
-    if (t + 1 < nkt) load_tile(t + 1);
+    load_tile(t + 1);  // past the last tile: range-checked zeros, never used
     const int64_t k0 = (int64_t)t * BN;
     if (k0 < kend_w) {
       const uint16_t* kb = Ks + buf * C::LDS_K;
@@ -281,8 +304,19 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
   const float* kg = reinterpret_cast<const float*>(p.k) + bw.b * p.ks[0] + bw.h * p.ks[2];
   const float* vg = reinterpret_cast<const float*>(p.v) + bw.b * p.vs[0] + bw.h * p.vs[2];
 
-  // Q: lane (query li, half hf) holds dims 4t+2hf and 4t+2hf+1.
   const int64_t row = bw.q0 + 32 * wv + li;
+  const int64_t kend_blk = p.causal ? min<int64_t>(S, bw.q0 + kBM + diag) : S;
+  const int nkt = kend_blk > 0 ? (int)cdiv(kend_blk, BN) : 0;
+  if (nkt == 0) {  // every row of the block sees no key: exactly 0
+    if (row < L) {
+      float* og = reinterpret_cast<float*>(p.out) + ((bw.b * L + row) * p.heads + bw.h) * E;
+#pragma unroll
+      for (int d = 0; d < E / 2; d += 4) *reinterpret_cast<f32x4*>(og + (E / 2) * hf + d) = f32x4{0, 0, 0, 0};
+    }
+    return;
+  }
+
+  // Q: lane (query li, half hf) holds dims 4t+2hf and 4t+2hf+1.
   float qr[E / 2];
 #pragma unroll
   for (int t = 0; t < E / 4; ++t) {
@@ -292,25 +326,29 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
     qr[2 * t + 1] = __uint_as_float(v.y);
   }
 
-  const int64_t kend_blk = p.causal ? min<int64_t>(S, bw.q0 + kBM + diag) : S;
-  const int nkt = kend_blk > 0 ? (int)cdiv(kend_blk, BN) : 0;
   const int64_t r0w = bw.q0 + 32 * wv;
   const int64_t kend_w = p.causal ? min<int64_t>(S, r0w + 32 + diag) : S;
 
+  // Global -> register staging through buffer loads rebased at each tile (fixed
+  // per-lane offsets; rows past S read as zeros).
   u32x4 kreg[C::CH], vreg[C::CH];
+  int koff[C::CH], voff[C::CH];
+#pragma unroll
+  for (int i = 0; i < C::CH; ++i) {
+    const int c = tid + 256 * i;
+    const int r = c / (E / 4), c4 = c % (E / 4);
+    koff[i] = (int)((r * p.ks[1] + 4 * c4) * 4);
+    voff[i] = (int)((r * p.vs[1] + 4 * c4) * 4);
+  }
   auto load_tile = [&](int t) {
     const int64_t k0 = (int64_t)t * BN;
+    const int64_t kbytes = ((S - 1 - k0) * p.ks[1] + E) * 4, vbytes = ((S - 1 - k0) * p.vs[1] + E) * 4;
+    const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kg + k0 * p.ks[1], kbytes);
+    const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vg + k0 * p.vs[1], vbytes);
 #pragma unroll
     for (int i = 0; i < C::CH; ++i) {
-      const int c = tid + 256 * i;
-      const int r = c / (E / 4), c4 = c % (E / 4);
-      u32x4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-      if (k0 + r < S) {
-        kv = *reinterpret_cast<const u32x4*>(kg + (k0 + r) * p.ks[1] + 4 * c4);
-        vv = *reinterpret_cast<const u32x4*>(vg + (k0 + r) * p.vs[1] + 4 * c4);
-      }
-      kreg[i] = kv;
-      vreg[i] = vv;
+      kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0);
+      vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, 0);
     }
   };
   auto store_tile = [&](int buf) {
@@ -331,14 +369,12 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
   float m_run = -INFINITY, l_run = 0.f;
   const float c = p.c;
 
-  if (nkt > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  load_tile(0);
+  store_tile(0);
   __syncthreads();
   for (int t = 0; t < nkt; ++t) {
     const int buf = t & 1;
-    if (t + 1 < nkt) load_tile(t + 1);
+    load_tile(t + 1);  // past the last tile: range-checked zeros, never used
     const int64_t k0 = (int64_t)t * BN;
     if (k0 < kend_w) {
       const float* kb = Ks + buf * C::LDS_K;
@@ -387,7 +423,7 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
           oacc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[key * VS + 32 * d + li], x[r], oacc[d], 0, 0, 0);
       }
     }
-    if (t + 1 < nkt) store_tile(buf ^ 1);
+    store_tile(buf ^ 1);
     __syncthreads();
   }
 
@@ -420,6 +456,12 @@ static int launch_lds(K kernel, int64_t nb, int lds, const FlashParams& p, hipSt
 int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
   const int64_t nb = p.batch * p.heads * cdiv(p.seq_q, kBM);
   if (nb == 0) return CA_OK;
+  // The tile loads address a tile's rows with 32-bit byte offsets from its first
+  // row: 64 rows of the token stride must fit (larger strides are declined and
+  // the caller copies the tensor).
+  const int64_t esz = bf16 ? 2 : 4;
+  const int64_t ts = p.ks[1] > p.vs[1] ? p.ks[1] : p.vs[1];
+  if (ts < 0 || 64 * (ts + E) * esz >= ((int64_t)1 << 31)) return CA_DECLINED;
   if (bf16) {
     switch (E) {
       case 32: return launch_lds(flash_bf16_kernel<32>, nb, FlashBf16Cfg<32>::LDS_BYTES, p, stream);
