@@ -195,39 +195,52 @@ __global__ __launch_bounds__(256, 2) void flash_bf16_kernel(FlashParams p) {
     if (k0 < kend_w) {
       const uint16_t* kb = Ks + buf * C::LDS_K;
       const uint16_t* vb = Vt + buf * C::LDS_V;
-      // S^T tiles: keys 0-31 and 32-63 of the tile.
-      f32x16 st[2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        st[kt] = f32x16{};
-#pragma unroll
-        for (int s = 0; s < E / 16; ++s) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(kb + (32 * kt + li) * KS + 16 * s + 8 * hf);
-          st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qr[s], st[kt], 0, 0, 0);
-        }
-      }
-      // Online softmax for query row r0w+li over the 32 keys this lane holds.
-      const bool need_mask = (k0 + BN > S) || (p.causal && k0 + BN - 1 > r0w + diag);
-      float x[2][16];
-      float mt = -INFINITY;
-      const int64_t lim = r0w + li + diag;
+      // S^T tiles: keys 0-31 and 32-63 of the tile.  All 2*E/16 A operands are read
+      // from LDS first, then the two accumulator chains are interleaved.
+      bf16x8 ka[2][E / 16];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float v = st[kt][r] * c;
-          if (need_mask) {
+        for (int s = 0; s < E / 16; ++s)
+          ka[kt][s] = *reinterpret_cast<const bf16x8*>(kb + (32 * kt + li) * KS + 16 * s + 8 * hf);
+      f32x16 st[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+      for (int s = 0; s < E / 16; ++s)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+          st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kt][s], qr[s], st[kt], 0, 0, 0);
+      // Online softmax for query row r0w+li over the 32 keys this lane holds: raw
+      // logits (masked keys -inf), row max in scaled log2 units as the reference
+      // takes it (tile max of the raw logits times c), p = 2^(s*c - m) with the
+      // scale folded into one FMA.  The running max is refreshed lazily: only when
+      // some row's tile max exceeds it by more than 8 (p stays below 2^8), which
+      // skips the accumulator rescale on most tiles; acc/l cancels it exactly.
+      const bool need_mask = (k0 + BN > S) || (p.causal && k0 + BN - 1 > r0w + diag);
+      float mt = -INFINITY;
+      if (need_mask) {
+        const int64_t lim = r0w + li + diag;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
             const int64_t j = k0 + 32 * kt + 8 * (r >> 2) + 4 * hf + (r & 3);
-            if (j >= S || (p.causal && j > lim)) v = -INFINITY;
+            if (j >= S || (p.causal && j > lim)) st[kt][r] = -INFINITY;
           }
-          x[kt][r] = v;
-          mt = fmaxf(mt, v);
-        }
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float m_new = fmaxf(m_run, mt);
-      const float mu = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - mu);
-      m_run = m_new;
+      }
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, st[kt][r]);
+      mt = fmaxf(mt, __shfl_xor(mt, 32)) * c;
+      if (__any(mt > m_run + 8.f)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < E / 32; ++d) oacc[d] *= alpha;
+        m_run = m_new;
+      }
+      const float mu = m_run == -INFINITY ? 0.f : m_run;
       float ls = 0.f;
       bf16x8 pb[4];
 #pragma unroll
@@ -235,26 +248,28 @@ __global__ __launch_bounds__(256, 2) void flash_bf16_kernel(FlashParams p) {
         uint32_t w[4];
 #pragma unroll
         for (int jj = 0; jj < 8; jj += 2) {
-          const float e0 = __builtin_amdgcn_exp2f(x[cc >> 1][8 * (cc & 1) + jj] - mu);
-          const float e1 = __builtin_amdgcn_exp2f(x[cc >> 1][8 * (cc & 1) + jj + 1] - mu);
+          const float e0 = __builtin_amdgcn_exp2f(fmaf(st[cc >> 1][8 * (cc & 1) + jj], c, -mu));
+          const float e1 = __builtin_amdgcn_exp2f(fmaf(st[cc >> 1][8 * (cc & 1) + jj + 1], c, -mu));
           ls += e0 + e1;
           w[jj / 2] = pack_bf16x2(e0, e1);
         }
         pb[cc] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
       }
-      l_run = l_run * alpha + ls;
-#pragma unroll
-      for (int d = 0; d < E / 32; ++d) oacc[d] *= alpha;
-      // O^T += V^T P^T
+      l_run += ls;
+      // O^T += V^T P^T: all V^T operands read first, then E/32 independent chains.
+      bf16x8 va[4][E / 32];
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
-        for (int d = 0; d < E / 32; ++d) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(vb + (32 * d + li) * VS + 16 * cc + 8 * hf);
-          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[cc], oacc[d], 0, 0, 0);
-        }
+        for (int d = 0; d < E / 32; ++d)
+          va[cc][d] = *reinterpret_cast<const bf16x8*>(vb + (32 * d + li) * VS + 16 * cc + 8 * hf);
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+        for (int d = 0; d < E / 32; ++d)
+          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[cc][d], pb[cc], oacc[d], 0, 0, 0);
     }
-    if (t + 1 < nkt) store_tile(buf ^ 1);
+    store_tile(buf ^ 1);  // past the last tile: zeros into the idle buffer
     __syncthreads();
   }
 
