@@ -5,29 +5,29 @@
 // tiles past the last visible key are never touched, the online softmax runs in
 // base 2 with c = scale*log2(e), and a row that sees no key is exactly 0.
 //
-// Block = 4 waves x 32 query rows.  Each wave keeps its Q rows in registers and
-// walks the key range in tiles staged through LDS (double-buffered; the next tile's
-// buffer loads are in flight while the current one is consumed, one barrier per
-// tile).  The loop body is branch-free around the loads: a conditional prefetch
-// made the compiler wait for it before the first MFMA of every tile.
-//
-//   S^T = K Q^T   32x32 MFMA tiles with keys as rows and queries as columns, so a
-//                 lane ends up owning one query and 16 keys of each tile;
-//   softmax       per lane (its query), with one cross-half exchange for the row max;
-//   O^T += V^T P^T the probabilities are already in the B-operand layout of the next
-//                 MFMA (no LDS round trip); V^T comes from LDS, where it is stored
-//                 transposed with bits 2 and 3 of the key index swapped so each lane's
-//                 8 keys are one 16-byte read.
-//
-// bf16: v_mfma_f32_32x32x16_bf16, P rounded to bf16 for P.V (as the reference's
-// bf16 policy does, flash_vec.mojo:255-259), fp32 accumulation.
-// fp32: v_mfma_f32_32x32x2_f32, everything fp32.
+// bf16 (flash_bf16_kernel): 8 waves x 32 query rows per block, one block per CU,
+// so each SIMD runs two waves, which take turns between MFMA work and softmax
+// work (ping-pong; a wave's own VALU and MFMA work do not overlap).  Key tiles
+// of 64 go global -> LDS with direct buffer loads two tiles ahead; K is read
+// with ds_read_b128, V^T with ds_read_b64_tr_b16 from the row-major V tile.
+//   S^T = K Q^T   32x32x16 MFMAs with keys as rows and queries as columns, so a
+//                 lane ends up owning one query and 16 keys of each 32-key half;
+//   softmax       per lane (its query) against a max fixed at the first tile;
+//                 rows whose later logits outgrow it by more than 2^20 are redone
+//                 by a safe pass with a running max;
+//   O^T += V^T P^T the probabilities are already in the B-operand layout of the
+//                 MFMA (no LDS round trip); P is rounded to bf16 as the reference's
+//                 bf16 policy does (flash_vec.mojo:255-259), fp32 accumulation.
+// fp32 (flash_f32_kernel): 4 waves x 32 rows, K/V staged through registers into
+// LDS, v_mfma_f32_32x32x2_f32, everything fp32.
+#include <type_traits>
+
 #include "ca_device.h"
 #include "ca_internal.h"
 
 namespace ca {
 
-constexpr int kBM = 128;  // query rows per block (4 waves x 32)
+constexpr int kBM = 128;  // fp32: query rows per block (4 waves x 32)
 
 // A raw buffer resource over [base, base + bytes): loads past `bytes` return 0.
 // The per-tile K/V loads rebase the resource at each tile, so their per-lane
@@ -70,222 +70,484 @@ __device__ __forceinline__ BlockWork block_work(const FlashParams& p) {
 // ---------------------------------------------------------------------------
 // bf16
 // ---------------------------------------------------------------------------
+// Block = 8 waves x 32 query rows, one block per CU, i.e. two waves per SIMD:
+// a wave's own VALU work does not overlap its own MFMAs on CDNA4, so the
+// softmax of one wave runs while the other wave's MFMAs do.  Key tiles of 64
+// go from global memory straight into LDS (buffer loads with LDS as the
+// destination: no staging registers; rows past the block's key range fill with
+// zeros), double-buffered.
+//
+// LDS layouts: rows of E bf16 padded to RSK (K) or RSV (V) 16-byte chunks, so
+// operand reads are conflict-free and every address is a per-lane base plus a
+// constant.  The V^T MFMA operands come from ds_read_b64_tr_b16 on the row-major
+// V tile: it gives lane j of a 16-lane group column j of a 4-row x 16-column
+// block (4 keys of one dim).
 template <int E>
 struct FlashBf16Cfg {
-  static constexpr int BN = 64;          // keys per tile
-  static constexpr int KS = E + 8;       // K row stride in LDS (elements): conflict-free reads
-  static constexpr int VS = BN + 8;      // V^T row stride
-  static constexpr int KCH = BN * E / 8 / 256;  // 16-byte K chunks per thread
-  static constexpr int VBLK = (BN / 4) * (E / 8);  // 4-key x 8-dim V blocks per tile
-  static constexpr int LDS_K = BN * KS;  // elements per K buffer
-  static constexpr int LDS_V = E * VS;
-  static constexpr int LDS_BYTES = 2 * (LDS_K + LDS_V) * 2;
+  static constexpr int NW = 8;             // waves per block
+  static constexpr int BM = 32 * NW;       // query rows per block
+  static constexpr int BN = 64;            // keys per tile
+  static constexpr int CPR = E / 8;        // 16-byte chunks per row
+  // Padded row strides in chunks.  K: 16 lanes reading one 16-byte column of 16
+  // consecutive rows hit 16 different 4-bank groups.  V: the 32 lanes that a
+  // transposed read serves together read 4 rows x two 32-byte segments; a stride
+  // of 4 or 12 chunks mod 16 puts the 4 rows 16 banks apart, so the 8 segments
+  // cover the 64 banks once.
+  static constexpr int RSK = CPR + 1;
+  static constexpr int RSV = CPR == 16 ? 20 : (CPR == 8 ? 12 : 4);
+  // Direct loads per thread and tile: every load of a wave fills 64 consecutive
+  // chunks, so a tile buffer is a whole number of NW x 64-chunk rounds (every
+  // wave issues the same number, so waits can count them).
+  static constexpr int NLK = (BN * RSK + 64 * NW - 1) / (64 * NW);
+  static constexpr int NLV = (BN * RSV + 64 * NW - 1) / (64 * NW);
+  static constexpr int KBUF = NLK * 64 * NW * 8;  // elements per K buffer
+  static constexpr int VBUF = NLV * 64 * NW * 8;
+  static constexpr int NBUF = 3;                  // loads run two tiles ahead
+  static constexpr int LDS_BYTES = NBUF * (KBUF + VBUF) * 2;
 };
 
-// Position of key k (0..63) in a V^T row: bits 2 and 3 swapped.
-__device__ __forceinline__ int vt_pos(int k) {
-  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4v;
+typedef __attribute__((address_space(3))) bf16x4v lds_bf16x4;
+
+// One bf16 block's work: a (batch, head) and one or two query blocks.  Causal
+// calls pair query block j with nqb-1-j, so every block walks about the same
+// number of key tiles (the expensive one first); non-causal blocks take one.
+struct PairWork {
+  int64_t b, h, qb0, qb1;
+  int n;
+};
+
+__device__ __forceinline__ PairWork pair_work(const FlashParams& p, int bm) {
+  const int64_t nqb = cdiv(p.seq_q, bm);
+  const int64_t per = p.causal ? (nqb + 1) / 2 : nqb;
+  const int64_t lg = xcd_remap(blockIdx.x, p.batch * p.heads * per);
+  const int64_t bh = lg / per, j = lg - bh * per;
+  PairWork w;
+  w.b = bh / p.heads;
+  w.h = bh - w.b * p.heads;
+  w.qb0 = p.causal ? nqb - 1 - j : j;
+  w.qb1 = j;
+  w.n = (p.causal && w.qb0 != j) ? 2 : 1;
+  return w;
+}
+
+// What one pass (a query block of one (batch, head)) needs, shared by the fast
+// walk and the safe pass.
+struct Bf16Pass {
+  const uint16_t* q;  // row 0 of the (batch, head)
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* out;      // row 0 of the (batch, head); rows H*E apart
+  int L, S, diag, q0, kend;
+  int qs1, ks1, vs1, heads;
+  float c;
+  int causal;
+};
+
+// Fixed per-thread byte offsets of the direct loads of a tile: load i of wave w
+// fills LDS chunk P = (NW*i + w)*64 + lane, i.e. row P / RS, column P % RS.  Pad
+// columns and chunks past the tile's rows get an offset past any window, so they
+// read as zeros without touching memory.
+template <int E, int RS, int NL>
+__device__ __forceinline__ void tile_offsets(int wv, int lane, int stride, int (&off)[NL]) {
+  constexpr int CPR = E / 8, BN = FlashBf16Cfg<E>::BN, NW = FlashBf16Cfg<E>::NW;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int P = (NW * i + wv) * 64 + lane, r = P / RS, col = P % RS;
+    off[i] = (r < BN && col < CPR) ? (r * stride + 8 * col) * 2 : (int)0x80000000;
+  }
+}
+
+// Fills one K or V tile buffer: rows [k0, k0 + BN) of the source, cut at the
+// pass's key range (rows past it read as zeros, a tile past it touches no memory).
+// The loads are issued from inline assembly: the compiler does not track them,
+// so it inserts no wait for them before unrelated LDS reads (it cannot tell the
+// buffers apart); loads_done_barrier() waits for them explicitly.
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+template <int E, int RS, int NL>
+__device__ __forceinline__ void fill_tile(uint16_t* buf, const uint16_t* src, int stride, int k0, int kend, int wv,
+                                          const int (&off)[NL]) {
+  constexpr int NW = FlashBf16Cfg<E>::NW;
+  const uint64_t addr = reinterpret_cast<uint64_t>(src + (int64_t)k0 * stride);
+  int64_t bytes = ((int64_t)(kend - 1 - k0) * stride + E) * 2;
+  bytes = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
+  // (wave-uniform values; readfirstlane keeps them in scalar registers even
+  // where the compiler cannot prove uniformity)
+  const i32x4 rs = {__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
+                    __builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffff)),
+                    __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>((lds_void*)buf));
+#pragma unroll
+  for (int i = 0; i < NL; ++i)
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds + (NW * i + wv) * 1024), "v"(off[i]), "s"(rs)
+                 : "memory");
+}
+
+// Waits until at most N of this wave's memory loads are outstanding (loads
+// complete in issue order), then the block barrier.
+template <int N>
+__device__ __forceinline__ void loads_landed_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+  __syncthreads();
+}
+__device__ __forceinline__ void loads_done_barrier() { loads_landed_barrier<0>(); }
+
+// K operand of the S MFMA: dims 16s + 8hf..+7 of key row `row`.
+template <int E>
+__device__ __forceinline__ bf16x8 k_operand(const uint16_t* kb, int row, int s, int hf) {
+  return *reinterpret_cast<const bf16x8*>(kb + (row * FlashBf16Cfg<E>::RSK + 2 * s + hf) * 8);
+}
+
+// V^T operand of the P.V MFMA for keys 16cc.. and dims 32d..: lane (dim li, half
+// hf) gets keys 16cc + 4hf + 0..3 and 16cc + 8 + 4hf + 0..3 (the order in which
+// the probabilities sit in the B operand).
+template <int E>
+__device__ __forceinline__ bf16x8 v_operand(const uint16_t* vb, int lane, int cc, int d) {
+  constexpr int RSV = FlashBf16Cfg<E>::RSV;
+  const int j = lane & 15, dh = (lane >> 4) & 1, hf = lane >> 5;
+  const uint16_t* base = vb + (4 * hf + (j >> 2)) * RSV * 8 + 16 * dh + 4 * (j & 3);
+  bf16x4v a[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    a[q] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + (16 * cc + 8 * q) * RSV * 8 + 32 * d));
+  return bf16x8{a[0][0], a[0][1], a[0][2], a[0][3], a[1][0], a[1][1], a[1][2], a[1][3]};
+}
+
+// -inf for keys past the row's limit (an arithmetic mask: a compare per element
+// would take a scalar mask register each).
+__device__ __forceinline__ float mask_key(float v, int vis, int key) {
+  int msk;
+  asm("v_ashrrev_i32 %0, 31, %1" : "=v"(msk) : "v"(vis - key));
+  return v + __int_as_float(msk & (int)0xff800000u);
+}
+
+// Per-wave state and the pieces of the key-tile step shared by the fast walk
+// and the safe pass: 32 query rows of one (batch, head), lane (query li, half
+// hf).
+template <int E>
+struct Bf16Rows {
+  static constexpr int BN = FlashBf16Cfg<E>::BN, NS = E / 16, ND = E / 32;
+  bf16x8 qr[NS];  // Q rows as B operands: dims 16s + 8hf..+7
+  f32x16 o[ND];   // O^T accumulators: dims 32d + 8(r/4) + 4hf + r%4
+  float m, l;
+  int li, hf, lane, r0;
+
+  __device__ __forceinline__ void load_q(const Bf16Pass& a) {
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(a.q + (int64_t)r0 * a.qs1, ((int64_t)(a.L - 1 - r0) * a.qs1 + E) * 2);
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      qr[s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (li * a.qs1 + 16 * s + 8 * hf) * 2, 0, 0));
+#pragma unroll
+    for (int d = 0; d < ND; ++d) o[d] = f32x16{};
+    m = -INFINITY;
+    l = 0.f;
+  }
+
+  // Keys of tile t this lane's row may see: key 32kt + 8(r/4) + 4hf + r%4 of the
+  // tile is visible when 32kt + 8(r/4) + r%4 <= the returned limit.
+  __device__ __forceinline__ int vis_of(const Bf16Pass& a, int t) const {
+    const int k0 = t * BN;
+    int lim = a.S - 1 - k0;
+    if (a.causal) lim = min(lim, r0 + li + a.diag - k0);
+    return max(-1, min(lim, BN)) - 4 * hf;
+  }
+
+  // S^T = K Q^T for the tile: keys as rows, queries as columns, so a lane ends
+  // up with one query and 16 keys of each 32-key half (two independent chains).
+  __device__ __forceinline__ void logits(const uint16_t* kb, f32x16 (&st)[2]) const {
+    f32x16 a0 = f32x16{}, a1 = f32x16{};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      a0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_operand<E>(kb, li, s, hf), qr[s], a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_operand<E>(kb, 32 + li, s, hf), qr[s], a1, 0, 0, 0);
+    }
+    st[0] = a0;
+    st[1] = a1;
+  }
+
+  // Row max of the tile in scaled log2 units, as the reference takes it (tile
+  // max of the visible raw logits times c).
+  __device__ __forceinline__ float tile_max(const f32x16 (&st)[2], int vis, float c) const {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, mask_key(st[kt][r], vis, 32 * kt + 8 * (r >> 2) + (r & 3)));
+    return fmaxf(mx, __shfl_xor(mx, 32)) * c;
+  }
+
+  // p = 2^(s*c - m), rounded to bf16 for P.V as the reference's bf16 policy does
+  // (flash_vec.mojo:255-259; l sums the unrounded p).  The 8 probabilities a lane
+  // holds per 16 keys are exactly the B operand of the P.V MFMA.  Returns the
+  // largest p as bits (positive floats order as integers).
+  template <bool MASK>
+  __device__ __forceinline__ uint32_t softmax(const f32x16 (&st)[2], int vis, float c, bf16x8 (&pb)[4]) {
+    const float nmu = m == -INFINITY ? 0.f : -m;
+    float ls = 0.f;
+    uint32_t pmax = 0;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      uint32_t w[4];
+#pragma unroll
+      for (int jj = 0; jj < 8; jj += 2) {
+        const int kt = cc >> 1, r = 8 * (cc & 1) + jj;
+        float v0 = st[kt][r], v1 = st[kt][r + 1];
+        if (MASK) {
+          v0 = mask_key(v0, vis, 32 * kt + 8 * (r >> 2) + (r & 3));
+          v1 = mask_key(v1, vis, 32 * kt + 8 * ((r + 1) >> 2) + ((r + 1) & 3));
+        }
+        const float e0 = __builtin_amdgcn_exp2f(fmaf(v0, c, nmu));
+        const float e1 = __builtin_amdgcn_exp2f(fmaf(v1, c, nmu));
+        pmax = max(pmax, max(__float_as_uint(e0), __float_as_uint(e1)));
+        ls += e0 + e1;
+        w[jj / 2] = pack_bf16x2(e0, e1);
+      }
+      pb[cc] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
+    }
+    l += ls;
+    return pmax;
+  }
+
+  // O^T += V^T P^T.
+  __device__ __forceinline__ void pv(const uint16_t* vb, const bf16x8 (&pb)[4]) {
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_operand<E>(vb, lane, cc, d), pb[cc], o[d], 0, 0, 0);
+  }
+
+  // One MFMA phase of the ping-pong walk: O^T += V^T P^T for the previous tile
+  // (PV, from vb and pb) and S^T = K Q^T for the next one (S, from kb into st),
+  // as one stream of MFMAs whose LDS operand reads run LA operands ahead, in
+  // scheduling regions of 4 MFMAs.  The lookahead keeps the LDS latency off the
+  // MFMA pipe; the regions keep the compiler from hoisting every read (which
+  // would not fit in a wave's 256 registers).
+  template <bool PV, bool S>
+  __device__ __forceinline__ void mfma_phase(const uint16_t* vb, const bf16x8 (&pb)[4], const uint16_t* kb,
+                                             f32x16 (&st)[2]) {
+    constexpr int NPV = PV ? 4 * ND : 0, NOP = NPV + (S ? 2 * NS : 0), LA = 8, R = LA + 1;
+    bf16x8 buf[R];
+    auto read = [&](int i) {
+      if (i < NPV) return v_operand<E>(vb, lane, i / ND, i % ND);
+      const int j = i - NPV;
+      return k_operand<E>(kb, 32 * (j & 1) + li, j >> 1, hf);
+    };
+#pragma unroll
+    for (int i = 0; i < NOP + LA; ++i) {
+      if (i < NOP) buf[i % R] = read(i);
+      const int k = i - LA;
+      if (k >= 0) {
+        if (k < NPV) {
+          o[k % ND] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(buf[k % R], pb[k / ND], o[k % ND], 0, 0, 0);
+        } else {
+          const int j = k - NPV, kt = j & 1, s = j >> 1;
+          st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(buf[k % R], qr[s], s == 0 ? f32x16{} : st[kt], 0, 0, 0);
+        }
+        if ((k & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
+  // out = acc / l; a row with no visible key is 0.
+  __device__ __forceinline__ void store(const Bf16Pass& a) const {
+    const float lt = l + __shfl_xor(l, 32);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    const int row = r0 + li;
+    if (row < a.L) {
+      uint16_t* orow = a.out + (int64_t)row * a.heads * E;
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          u32x2 w = {pack_bf16x2(o[d][4 * q] * inv, o[d][4 * q + 1] * inv),
+                     pack_bf16x2(o[d][4 * q + 2] * inv, o[d][4 * q + 3] * inv)};
+          *reinterpret_cast<u32x2*>(orow + 32 * d + 8 * q + 4 * hf) = w;
+        }
+    }
+  }
+};
+
+// The safe pass: a walk with a lazily refreshed running max (refreshed when a
+// tile max exceeds it by more than 8, the accumulators rescaled then; acc/l
+// cancels the choice of max).  Every wave of the block takes part in the loads
+// and barriers; waves with `active` false compute and store nothing.  Used for
+// the rows whose logits outgrew the fast walk's fixed max; it is kept out of
+// line so that its registers do not constrain the fast walk's.
+template <int E>
+__device__ __noinline__ void bf16_safe_pass(const Bf16Pass& a, bool active) {
+  using C = FlashBf16Cfg<E>;
+  constexpr int BN = C::BN, ND = E / 32;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* Ks = smem;
+  uint16_t* Vs = smem + C::NBUF * C::KBUF;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  Bf16Rows<E> w;
+  w.lane = lane;
+  w.li = lane & 31;
+  w.hf = lane >> 5;
+  w.r0 = a.q0 + 32 * wv;
+  int koff[C::NLK], voff[C::NLV];
+  tile_offsets<E, C::RSK>(wv, lane, a.ks1, koff);
+  tile_offsets<E, C::RSV>(wv, lane, a.vs1, voff);
+  const int nkt = a.kend > 0 ? (a.kend + BN - 1) / BN : 0;
+  const int kend_w = a.causal ? min(a.S, w.r0 + 32 + a.diag) : a.S;
+  const int nkt_w = active && kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
+  w.load_q(a);
+
+  __syncthreads();  // the fast walk is done with the tile buffers
+  for (int t = 0; t < nkt; ++t) {
+    fill_tile<E, C::RSK>(Ks, a.k, a.ks1, t * BN, a.kend, wv, koff);
+    fill_tile<E, C::RSV>(Vs, a.v, a.vs1, t * BN, a.kend, wv, voff);
+    loads_done_barrier();
+    if (t < nkt_w) {
+      f32x16 st[2];
+      w.logits(Ks, st);
+      const int vis = w.vis_of(a, t);
+      const float mt = w.tile_max(st, vis, a.c);
+      if (__any(mt > w.m + 8.f)) {
+        const float mn = fmaxf(w.m, mt);
+        const float alpha = __builtin_amdgcn_exp2f(w.m - (mn == -INFINITY ? 0.f : mn));
+        w.l *= alpha;
+#pragma unroll
+        for (int d = 0; d < ND; ++d) w.o[d] *= alpha;
+        w.m = mn;
+      }
+      bf16x8 pb[4];
+      w.template softmax<true>(st, vis, a.c, pb);
+      w.pv(Vs, pb);
+    }
+    __syncthreads();  // every wave is done with the tiles before they are refilled
+  }
+  if (active) w.store(a);
 }
 
 template <int E>
-__global__ __launch_bounds__(256, 2) void flash_bf16_kernel(FlashParams p) {
+__global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
   using C = FlashBf16Cfg<E>;
-  constexpr int BN = C::BN, KS = C::KS, VS = C::VS;
+  constexpr int BM = C::BM, BN = C::BN;
+  // Headroom of the fast walk's fixed max: p <= 2^20 (a NaN p also exceeds it).
+  constexpr uint32_t kHeadBits = 0x49800000u;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* Ks = smem;                  // [2][BN][KS]
-  uint16_t* Vt = smem + 2 * C::LDS_K;   // [2][E][VS]
+  uint16_t* Ks = smem;                      // Kbuf[NBUF]
+  uint16_t* Vs = smem + C::NBUF * C::KBUF;  // Vbuf[NBUF]
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int li = lane & 31, hf = lane >> 5;
-  const BlockWork bw = block_work(p);
-  const int64_t L = p.seq_q, S = p.seq_k, diag = S - L;
-  const uint16_t* qg = reinterpret_cast<const uint16_t*>(p.q) + bw.b * p.qs[0] + bw.h * p.qs[2];
-  const uint16_t* kg = reinterpret_cast<const uint16_t*>(p.k) + bw.b * p.ks[0] + bw.h * p.ks[2];
-  const uint16_t* vg = reinterpret_cast<const uint16_t*>(p.v) + bw.b * p.vs[0] + bw.h * p.vs[2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches and windows
+  const PairWork pw = pair_work(p, BM);
+  // Positions and token strides fit 32 bits (the launcher declines otherwise).
+  Bf16Pass a;
+  a.L = (int)p.seq_q;
+  a.S = (int)p.seq_k;
+  a.diag = a.S - a.L;
+  a.qs1 = (int)p.qs[1];
+  a.ks1 = (int)p.ks[1];
+  a.vs1 = (int)p.vs[1];
+  a.heads = (int)p.heads;
+  a.c = p.c;
+  a.causal = p.causal;
+  a.q = reinterpret_cast<const uint16_t*>(p.q) + pw.b * p.qs[0] + pw.h * p.qs[2];
+  a.k = reinterpret_cast<const uint16_t*>(p.k) + pw.b * p.ks[0] + pw.h * p.ks[2];
+  a.v = reinterpret_cast<const uint16_t*>(p.v) + pw.b * p.vs[0] + pw.h * p.vs[2];
+  a.out = reinterpret_cast<uint16_t*>(p.out) + (pw.b * p.seq_q * p.heads + pw.h) * E;
+  const int S = a.S, diag = a.diag;
+  int koff[C::NLK], voff[C::NLV];
+  tile_offsets<E, C::RSK>(wv, lane, a.ks1, koff);
+  tile_offsets<E, C::RSV>(wv, lane, a.vs1, voff);
 
-  const int64_t row = bw.q0 + 32 * wv + li;
-  const int64_t kend_blk = p.causal ? min<int64_t>(S, bw.q0 + kBM + diag) : S;
-  const int nkt = kend_blk > 0 ? (int)cdiv(kend_blk, BN) : 0;
-  if (nkt == 0) {  // every row of the block sees no key: exactly 0
-    if (row < L) {
-      uint16_t* og = reinterpret_cast<uint16_t*>(p.out) + ((bw.b * L + row) * p.heads + bw.h) * E;
-#pragma unroll
-      for (int d = 0; d < E / 2; d += 8) *reinterpret_cast<u32x4*>(og + (E / 2) * hf + d) = u32x4{0, 0, 0, 0};
-    }
-    return;
-  }
+  Bf16Rows<E> w;
+  w.lane = lane;
+  w.li = lane & 31;
+  w.hf = lane >> 5;
 
-  // Q rows of this wave as B operands: lane (query li, half hf) holds dims 16s+8hf..+7.
-  bf16x8 qr[E / 16];
-#pragma unroll
-  for (int s = 0; s < E / 16; ++s) {
-    u32x4 v = {0, 0, 0, 0};
-    if (row < L) v = *reinterpret_cast<const u32x4*>(qg + row * p.qs[1] + 16 * s + 8 * hf);
-    qr[s] = __builtin_bit_cast(bf16x8, v);
-  }
+  for (int pass = 0; pass < pw.n; ++pass) {
+    const int q0 = (int)(pass == 0 ? pw.qb0 : pw.qb1) * BM;
+    w.r0 = q0 + 32 * wv;  // first row of this wave
+    const int kend_b = p.causal ? min(S, q0 + BM + diag) : S;
+    const int nkt = kend_b > 0 ? (kend_b + BN - 1) / BN : 0;
+    const int kend_w = p.causal ? min(S, w.r0 + 32 + diag) : S;
+    const int nkt_w = kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
+    a.q0 = q0;
+    a.kend = kend_b;
 
-  const int64_t r0w = bw.q0 + 32 * wv;  // first row of this wave
-  const int64_t kend_w = p.causal ? min<int64_t>(S, r0w + 32 + diag) : S;
+    if (pass > 0) __syncthreads();  // every wave is done with the previous pass's tiles
+    w.load_q(a);
+    bool bad = false;
 
-  // Global -> register staging of one K/V tile through buffer loads: fixed per-lane
-  // byte offsets, the resource rebased at the tile; rows past S read as zeros.
-  u32x4 kreg[C::KCH];
-  u32x4 vreg[4];
-  int koff[C::KCH], voff[4];
-#pragma unroll
-  for (int i = 0; i < C::KCH; ++i) {
-    const int c = tid + 256 * i;
-    koff[i] = (int)(((c / (E / 8)) * p.ks[1] + 8 * (c % (E / 8))) * 2);
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) voff[r] = (int)(((4 * (tid & 15) + r) * p.vs[1] + 8 * (tid >> 4)) * 2);
-  auto load_tile = [&](int t) {
-    const int64_t k0 = (int64_t)t * BN;
-    const int64_t kbytes = ((S - 1 - k0) * p.ks[1] + E) * 2, vbytes = ((S - 1 - k0) * p.vs[1] + E) * 2;
-    const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kg + k0 * p.ks[1], kbytes);
-    const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vg + k0 * p.vs[1], vbytes);
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0);
-    if (C::VBLK >= 256 || tid < C::VBLK) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) vreg[r] = __builtin_amdgcn_raw_buffer_load_b128(vr, voff[r], 0, 0);
-    }
-  };
-  auto store_tile = [&](int buf) {
-    uint16_t* kb = Ks + buf * C::LDS_K;
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int c = tid + 256 * i;
-      const int r = c / (E / 8), c8 = c % (E / 8);
-      *reinterpret_cast<u32x4*>(kb + r * KS + 8 * c8) = kreg[i];
-    }
-    if (C::VBLK >= 256 || tid < C::VBLK) {
-      const int kgp = tid & 15, dc = tid >> 4;
-      uint16_t* vb = Vt + buf * C::LDS_V + (8 * dc) * VS + vt_pos(4 * kgp);
-      const uint32_t w0[4] = {vreg[0].x, vreg[0].y, vreg[0].z, vreg[0].w};
-      const uint32_t w1[4] = {vreg[1].x, vreg[1].y, vreg[1].z, vreg[1].w};
-      const uint32_t w2[4] = {vreg[2].x, vreg[2].y, vreg[2].z, vreg[2].w};
-      const uint32_t w3[4] = {vreg[3].x, vreg[3].y, vreg[3].z, vreg[3].w};
-#pragma unroll
-      for (int d2 = 0; d2 < 4; ++d2) {
-        // dims 2*d2 (low halves) and 2*d2+1 (high halves) of keys 0..3
-        u32x2 lo = {(w0[d2] & 0xffffu) | (w1[d2] << 16), (w2[d2] & 0xffffu) | (w3[d2] << 16)};
-        u32x2 hi = {(w0[d2] >> 16) | (w1[d2] & 0xffff0000u), (w2[d2] >> 16) | (w3[d2] & 0xffff0000u)};
-        *reinterpret_cast<u32x2*>(vb + (2 * d2) * VS) = lo;
-        *reinterpret_cast<u32x2*>(vb + (2 * d2 + 1) * VS) = hi;
-      }
-    }
-  };
-
-  f32x16 oacc[E / 32];
-#pragma unroll
-  for (int d = 0; d < E / 32; ++d) oacc[d] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.f;
-  const float c = p.c;
-
-  if (nkt > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-  for (int t = 0; t < nkt; ++t) {
-    const int buf = t & 1;
-    load_tile(t + 1);  // past the last tile: range-checked zeros, never used
-    const int64_t k0 = (int64_t)t * BN;
-    if (k0 < kend_w) {
-      const uint16_t* kb = Ks + buf * C::LDS_K;
-      const uint16_t* vb = Vt + buf * C::LDS_V;
-      // S^T tiles: keys 0-31 and 32-63 of the tile.  All 2*E/16 A operands are read
-      // from LDS first, then the two accumulator chains are interleaved.
-      bf16x8 ka[2][E / 16];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int s = 0; s < E / 16; ++s)
-          ka[kt][s] = *reinterpret_cast<const bf16x8*>(kb + (32 * kt + li) * KS + 16 * s + 8 * hf);
-      f32x16 st[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-      for (int s = 0; s < E / 16; ++s)
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-          st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kt][s], qr[s], st[kt], 0, 0, 0);
-      // Online softmax for query row r0w+li over the 32 keys this lane holds: raw
-      // logits (masked keys -inf), row max in scaled log2 units as the reference
-      // takes it (tile max of the raw logits times c), p = 2^(s*c - m) with the
-      // scale folded into one FMA.  The running max is refreshed lazily: only when
-      // some row's tile max exceeds it by more than 8 (p stays below 2^8), which
-      // skips the accumulator rescale on most tiles; acc/l cancels it exactly.
-      const bool need_mask = (k0 + BN > S) || (p.causal && k0 + BN - 1 > r0w + diag);
-      float mt = -INFINITY;
-      if (need_mask) {
-        const int64_t lim = r0w + li + diag;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int64_t j = k0 + 32 * kt + 8 * (r >> 2) + 4 * hf + (r & 3);
-            if (j >= S || (p.causal && j > lim)) st[kt][r] = -INFINITY;
-          }
-      }
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, st[kt][r]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32)) * c;
-      if (__any(mt > m_run + 8.f)) {
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
-        l_run *= alpha;
-#pragma unroll
-        for (int d = 0; d < E / 32; ++d) oacc[d] *= alpha;
-        m_run = m_new;
-      }
-      const float mu = m_run == -INFINITY ? 0.f : m_run;
-      float ls = 0.f;
+    // The fast walk.  The row max is fixed at tile 0's (every row that sees any
+    // key sees key 0) and never refreshed, so the loop touches the accumulators
+    // only through MFMAs; p stays below 2^20 unless a later logit exceeds the
+    // fixed max by more than 20 (log2 units), which `bad` records.
+    //
+    // Ping-pong: waves 0-3 (group 0) and 4-7 (group 1) share each SIMD and take
+    // turns, half a tile apart, between an MFMA phase (the S MFMAs of tile t and
+    // the P.V MFMAs of tile t-1) and a VALU phase (the softmax of tile t); a
+    // block barrier ends every half-step h.  Group g runs its MFMA phase for
+    // tile t at h = 2t + g and its softmax of tile t at h = 2t + g + 1, so K(t)
+    // is read at h = 2t, 2t+1 and V(t) at h = 2t+2, 2t+3.  Loads run two tiles
+    // ahead in three buffers: at even h = 2t every wave issues its share of the
+    // loads of K(t+2) and V(t+1) (into the buffers of K(t-1) and V(t-2), last
+    // read at h = 2t-1), and the barrier that ends h = 2t+1 waits for the loads
+    // issued at h = 2t-2 (K(t+1) and V(t)).
+    if (nkt > 0) {
+      constexpr int NL = C::NLK + C::NLV;  // direct loads per wave and tile
+      const int wg = wv >> 2;
+      f32x16 st[2];
       bf16x8 pb[4];
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) {
-        uint32_t w[4];
-#pragma unroll
-        for (int jj = 0; jj < 8; jj += 2) {
-          const float e0 = __builtin_amdgcn_exp2f(fmaf(st[cc >> 1][8 * (cc & 1) + jj], c, -mu));
-          const float e1 = __builtin_amdgcn_exp2f(fmaf(st[cc >> 1][8 * (cc & 1) + jj + 1], c, -mu));
-          ls += e0 + e1;
-          w[jj / 2] = pack_bf16x2(e0, e1);
+      for (int cc = 0; cc < 4; ++cc) pb[cc] = bf16x8{};
+      auto kbuf = [&](int t) { return Ks + (t % C::NBUF) * C::KBUF; };
+      auto vbuf = [&](int t) { return Vs + ((t + C::NBUF) % C::NBUF) * C::VBUF; };
+      fill_tile<E, C::RSK>(kbuf(0), a.k, a.ks1, 0, kend_b, wv, koff);
+      fill_tile<E, C::RSK>(kbuf(1), a.k, a.ks1, BN, kend_b, wv, koff);
+      fill_tile<E, C::RSV>(vbuf(0), a.v, a.vs1, 0, kend_b, wv, voff);
+      fill_tile<E, C::RSV>(vbuf(-1), a.v, a.vs1, 0, 0, wv, voff);  // zeros: an empty window
+      loads_done_barrier();
+      for (int h = 0; h < 2 * nkt + 2; ++h) {
+        if ((h & 1) == 0) {
+          const int t = h >> 1;
+          fill_tile<E, C::RSK>(kbuf(t + 2), a.k, a.ks1, (t + 2) * BN, kend_b, wv, koff);
+          fill_tile<E, C::RSV>(vbuf(t + 1), a.v, a.vs1, (t + 1) * BN, kend_b, wv, voff);
         }
-        pb[cc] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
+        if (((h + wg) & 1) == 0) {
+          const int t = (h - wg) >> 1;
+          // Phases at t = 0 (P.V with pb = 0 over a zero-filled V buffer) and
+          // t = nkt_w (S of a tile it does not use) run the same code.
+          if (t <= nkt_w && nkt_w > 0) {
+            __builtin_amdgcn_s_setprio(1);
+            w.template mfma_phase<true, true>(vbuf(t - 1), pb, kbuf(t), st);
+            __builtin_amdgcn_s_setprio(0);
+          }
+        } else {
+          const int t = (h - 1 - wg) >> 1;
+          if (t >= 0 && t < nkt_w) {
+            const int k0 = t * BN;
+            if (t == 0 || k0 + BN > S || (p.causal && k0 + BN - 1 > w.r0 + diag)) {
+              const int vis = w.vis_of(a, t);
+              if (t == 0) w.m = w.tile_max(st, vis, a.c);
+              bad |= w.template softmax<true>(st, vis, a.c, pb) > kHeadBits;
+            } else {
+              bad |= w.template softmax<false>(st, BN, a.c, pb) > kHeadBits;
+            }
+          }
+        }
+        if (h & 1)
+          loads_landed_barrier<NL>();
+        else
+          __syncthreads();
       }
-      l_run += ls;
-      // O^T += V^T P^T: all V^T operands read first, then E/32 independent chains.
-      bf16x8 va[4][E / 32];
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-        for (int d = 0; d < E / 32; ++d)
-          va[cc][d] = *reinterpret_cast<const bf16x8*>(vb + (32 * d + li) * VS + 16 * cc + 8 * hf);
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-        for (int d = 0; d < E / 32; ++d)
-          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[cc][d], pb[cc], oacc[d], 0, 0, 0);
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads past the range (zeros) have landed
     }
-    store_tile(buf ^ 1);  // past the last tile: zeros into the idle buffer
-    __syncthreads();
-  }
-
-  // Epilogue: out = acc / l; a row with no visible key is 0.
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (row < L) {
-    uint16_t* og = reinterpret_cast<uint16_t*>(p.out) + ((bw.b * L + row) * p.heads + bw.h) * E;
-#pragma unroll
-    for (int d = 0; d < E / 32; ++d)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        u32x2 w = {pack_bf16x2(oacc[d][4 * g] * inv, oacc[d][4 * g + 1] * inv),
-                   pack_bf16x2(oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv)};
-        *reinterpret_cast<u32x2*>(og + 32 * d + 8 * g + 4 * hf) = w;
-      }
+    bad = __any(bad);
+    // A wave whose fast walk recorded an overflow risk leaves its rows to the
+    // safe pass.
+    if (!bad) w.store(a);
+    if (__syncthreads_or(bad)) bf16_safe_pass<E>(a, bad);
   }
 }
 
@@ -457,37 +719,44 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
 }
 
 template <typename K>
-static int launch_lds(K kernel, int64_t nb, int lds, const FlashParams& p, hipStream_t stream) {
+static int launch_lds(K kernel, int64_t nb, int threads, int lds, const FlashParams& p, hipStream_t stream) {
   if (nb > 0x7fffffff) return CA_DECLINED;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return CA_HIP_ERROR - (int)e;
   }
-  hipLaunchKernelGGL(kernel, dim3((unsigned)nb), dim3(256), lds, stream, p);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)nb), dim3(threads), lds, stream, p);
   return ca_launch_status();
 }
 
 int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
-  const int64_t nb = p.batch * p.heads * cdiv(p.seq_q, kBM);
-  if (nb == 0) return CA_OK;
+  if (p.batch * p.heads * p.seq_q == 0) return CA_OK;
   // The tile loads address a tile's rows with 32-bit byte offsets from its first
   // row: 64 rows of the token stride must fit (larger strides are declined and
   // the caller copies the tensor).
   const int64_t esz = bf16 ? 2 : 4;
-  const int64_t ts = p.ks[1] > p.vs[1] ? p.ks[1] : p.vs[1];
-  if (ts < 0 || 64 * (ts + E) * esz >= ((int64_t)1 << 31)) return CA_DECLINED;
+  int64_t ts = p.ks[1] > p.vs[1] ? p.ks[1] : p.vs[1];
+  if (p.qs[1] > ts) ts = p.qs[1];
+  if (p.qs[1] < 0 || p.ks[1] < 0 || p.vs[1] < 0 || 64 * (ts + E) * esz >= ((int64_t)1 << 31))
+    return CA_DECLINED;
+  // Row and key positions are 32-bit inside the kernels.
+  if (p.seq_q >= ((int64_t)1 << 30) || p.seq_k >= ((int64_t)1 << 30)) return CA_DECLINED;
   if (bf16) {
+    // One block per (batch, head) and query-block pair (causal) or query block.
+    const int64_t nqb = cdiv(p.seq_q, FlashBf16Cfg<128>::BM);
+    const int64_t nb = p.batch * p.heads * (p.causal ? (nqb + 1) / 2 : nqb);
     switch (E) {
-      case 32: return launch_lds(flash_bf16_kernel<32>, nb, FlashBf16Cfg<32>::LDS_BYTES, p, stream);
-      case 64: return launch_lds(flash_bf16_kernel<64>, nb, FlashBf16Cfg<64>::LDS_BYTES, p, stream);
-      case 128: return launch_lds(flash_bf16_kernel<128>, nb, FlashBf16Cfg<128>::LDS_BYTES, p, stream);
+      case 32: return launch_lds(flash_bf16_kernel<32>, nb, 64 * FlashBf16Cfg<32>::NW, FlashBf16Cfg<32>::LDS_BYTES, p, stream);
+      case 64: return launch_lds(flash_bf16_kernel<64>, nb, 64 * FlashBf16Cfg<64>::NW, FlashBf16Cfg<64>::LDS_BYTES, p, stream);
+      case 128: return launch_lds(flash_bf16_kernel<128>, nb, 64 * FlashBf16Cfg<128>::NW, FlashBf16Cfg<128>::LDS_BYTES, p, stream);
     }
   } else {
+    const int64_t nb = p.batch * p.heads * cdiv(p.seq_q, kBM);
     switch (E) {
-      case 32: return launch_lds(flash_f32_kernel<32>, nb, FlashF32Cfg<32>::LDS_BYTES, p, stream);
-      case 64: return launch_lds(flash_f32_kernel<64>, nb, FlashF32Cfg<64>::LDS_BYTES, p, stream);
-      case 128: return launch_lds(flash_f32_kernel<128>, nb, FlashF32Cfg<128>::LDS_BYTES, p, stream);
+      case 32: return launch_lds(flash_f32_kernel<32>, nb, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream);
+      case 64: return launch_lds(flash_f32_kernel<64>, nb, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream);
+      case 128: return launch_lds(flash_f32_kernel<128>, nb, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream);
     }
   }
   return CA_DECLINED;

@@ -125,3 +125,24 @@ def test_cfg4_prefill_full_size_sampled(cuda):
         ref = (w / w.sum(-1, keepdims=True)) @ vb
         got = values(out[b, rows, h])
         assert np.abs(got - ref).max() <= 2e-2
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_logits_outgrowing_the_first_tile(cuda, d, causal):
+    """Keys far past the first 64 whose logits exceed every logit of the first key
+    tile by far more than 2^20 in probability: the bf16 kernel's fast walk keeps
+    the first tile's row max, so those rows must be recomputed with a running max
+    (some waves of a block take that path, others do not)."""
+    g = torch.Generator().manual_seed(11)
+    b, sq, sk, h = 2, 300, 700, 2
+    q = (torch.randn(b, sq, h, d, generator=g) + 1.0).bfloat16()
+    k = torch.randn(b, sk, h, d, generator=g)
+    k[:, 200] = 6.0  # q.k ~ 6d: ~68 (d=128) above the others after scaling
+    k[:, 650] = 5.0
+    k = k.bfloat16()
+    v = torch.randn(b, sk, h, d, generator=g).bfloat16()
+    q, k, v = q.to(cuda), k.to(cuda), v.to(cuda)
+    out = flash_attn_func(q, k, v, causal=causal)
+    ref = attention(values(q), values(k), values(v), d ** -0.5, causal)
+    assert_close(out, ref, torch.bfloat16, paged=False)
