@@ -19,6 +19,12 @@ the timed region (inputs already resident in HBM).  The JSON line also carries:
   reference cannot be built here) on the box's host cores, on a bounded sample
   of the same workload.
 
+``roofline.traffic`` is the HBM bytes one call moves, from rocprofv3 --pmc runs
+of ``python bench.py --profile-pass`` (one 1 GiB device copy, then one call of
+each workload): FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the
+same counter reads for the copy (TRAFFIC below; rerun the passes after a kernel
+change).
+
 Algorithmic bytes (decode) = sum over rows of 2*len*H*E*2 (K and V once) + q + out
 + page-table entries read + lengths; split-K partials are implementation traffic
 and are not counted.  Prefill FLOP = 4*E per visible (query, key) pair.
@@ -40,6 +46,21 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+COPY_BYTES = 1 << 30  # the calibration copy of --profile-pass
+
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of --profile-pass on
+# MI355X: the calibration copy, then the decode kernels and the prefill kernel.
+TRAFFIC = {
+    "copy": {"fetch_kib": 524308.6, "write_kib": 1048576.0},
+    "decode": {"fetch_kib": 543470.8 + 2379.0, "write_kib": 4796.9 + 424.0},  # tiles + combine
+    "prefill": {"fetch_kib": 321530.4, "write_kib": 174200.5},
+}
+
+
+def traffic_bytes(name):
+    """HBM bytes of one call: each counter scaled by its reading for a known copy."""
+    t, c = TRAFFIC[name], TRAFFIC["copy"]
+    return int(t["fetch_kib"] * COPY_BYTES / c["fetch_kib"] + t["write_kib"] * COPY_BYTES / c["write_kib"])
 METRIC = "decode HBM GB/s + µs/call; prefill TFLOP/s (bf16) vs MI355X roofline"
 
 
@@ -135,6 +156,35 @@ def cpu_prefill_baseline(budget_s=4.0):
                       f"(L=S=4096 E=128 causal bf16), {reps} calls, {dt * 1e3:.1f} ms/call"}
 
 
+def prefill_workload(dev):
+    N, L, H, E = 4, 4096, 32, 128
+    g = torch.Generator(device=dev).manual_seed(1)
+    qkv = torch.randn(N * L, 3 * H * E, generator=g, device=dev).to(torch.bfloat16)
+    q, k, v = (qkv[:, i * H * E:(i + 1) * H * E].view(N, L, H, E) for i in range(3))
+    return qkv, q, k, v
+
+
+def profile_pass(dev, mod, rt):
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    w = decode_workload(dev)
+    out = torch.empty_like(w["q"])
+    assert mod.decode(rt, w["q"], w["kc"], w["vc"], None, None, None, w["seqlens"], w["table"],
+                      None, out) is not None
+    torch.cuda.synchronize()
+    del w, out
+    torch.cuda.empty_cache()
+    qkv, q, k, v = prefill_workload(dev)
+    r = mod.flash(rt, q, k, v, None, True, 0, 0)
+    assert r is not None and not isinstance(r, int)
+    torch.cuda.synchronize()
+    print("profile pass done", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,6 +192,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill line")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="no timing: one 1 GiB device copy, one decode call and one prefill call "
+                         "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the ops run within one device and this build "
@@ -155,6 +208,10 @@ def main():
     torch.cuda.set_device(dev)
     mod, rt = K.module(), K.runtime()
     K.set_host_checks(False)  # no host reads inside the timed loop
+
+    if args.profile_pass:
+        profile_pass(dev, mod, rt)
+        return
 
     w = decode_workload(dev)
     out = torch.empty_like(w["q"])
@@ -179,7 +236,8 @@ def main():
         "us_per_call": round(call_ms * 1e3, 2),
         "us_per_call_median": round(float(np.median(ms)) * 1e3, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs_kernel, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs_kernel / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs_kernel / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_bytes("decode"),
                      "kernel": "decode_tiles_kernel<128,bf16> + decode_tiles_combine_kernel<128,bf16> (one call)",
                      "algorithmic_bytes": w["bytes"]},
     }
@@ -188,9 +246,7 @@ def main():
 
     if not args.no_prefill:
         N, L, H, E = 4, 4096, 32, 128
-        g = torch.Generator(device=dev).manual_seed(1)
-        qkv = torch.randn(N * L, 3 * H * E, generator=g, device=dev).to(torch.bfloat16)
-        q, k, v = (qkv[:, i * H * E:(i + 1) * H * E].view(N, L, H, E) for i in range(3))
+        qkv, q, k, v = prefill_workload(dev)
 
         def pstep():
             r = mod.flash(rt, q, k, v, None, True, 0, 0)
@@ -207,7 +263,7 @@ def main():
             "us_per_call": round(pcall * 1e3, 1),
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
-                         "traffic": None, "kernel": "flash_bf16_kernel<128>",
+                         "traffic": traffic_bytes("prefill"), "kernel": "flash_bf16_kernel<128>",
                          "algorithmic_flop": flop},
         }
         del qkv, q, k, v
