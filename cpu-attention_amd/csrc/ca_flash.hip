@@ -75,7 +75,9 @@ __device__ __forceinline__ BlockWork block_work(const FlashParams& p) {
 // softmax of one wave runs while the other wave's MFMAs do.  Key tiles of 64
 // go from global memory straight into LDS (buffer loads with LDS as the
 // destination: no staging registers; rows past the block's key range fill with
-// zeros), double-buffered.
+// zeros), three buffers deep.  The waves in their MFMA phase issue the loads
+// (group 0 the K tiles, group 1 the V tiles): their issue slots are idle while
+// the matrix pipe works, whereas the softmax phase is short of them.
 //
 // LDS layouts: rows of E bf16 padded to RSK (K) or RSV (V) 16-byte chunks, so
 // operand reads are conflict-free and every address is a per-lane base plus a
@@ -85,6 +87,7 @@ __device__ __forceinline__ BlockWork block_work(const FlashParams& p) {
 template <int E>
 struct FlashBf16Cfg {
   static constexpr int NW = 8;             // waves per block
+  static constexpr int NWG = 4;            // waves per ping-pong group
   static constexpr int BM = 32 * NW;       // query rows per block
   static constexpr int BN = 64;            // keys per tile
   static constexpr int CPR = E / 8;        // 16-byte chunks per row
@@ -95,15 +98,16 @@ struct FlashBf16Cfg {
   // cover the 64 banks once.
   static constexpr int RSK = CPR + 1;
   static constexpr int RSV = CPR == 16 ? 20 : (CPR == 8 ? 12 : 4);
-  // Direct loads per thread and tile: every load of a wave fills 64 consecutive
-  // chunks, so a tile buffer is a whole number of NW x 64-chunk rounds (every
-  // wave issues the same number, so waits can count them).
-  static constexpr int NLK = (BN * RSK + 64 * NW - 1) / (64 * NW);
-  static constexpr int NLV = (BN * RSV + 64 * NW - 1) / (64 * NW);
-  static constexpr int KBUF = NLK * 64 * NW * 8;  // elements per K buffer
-  static constexpr int VBUF = NLV * 64 * NW * 8;
-  static constexpr int NBUF = 3;                  // loads run two tiles ahead
-  static constexpr int LDS_BYTES = NBUF * (KBUF + VBUF) * 2;
+  // Direct loads per thread and tile: a group's 4 waves load a tile, every
+  // load of a wave fills 64 consecutive chunks, so a tile buffer is NL rounds
+  // of 4 x 64 chunks.  K and V tiles take the same NL (the larger), so every
+  // wave issues the same number of loads per tile and one wait count serves all.
+  static constexpr int NLK = (BN * RSK + 64 * NWG - 1) / (64 * NWG);
+  static constexpr int NLV = (BN * RSV + 64 * NWG - 1) / (64 * NWG);
+  static constexpr int NL = NLK > NLV ? NLK : NLV;
+  static constexpr int TBUF = NL * 64 * NWG * 8;  // elements per tile buffer
+  static constexpr int NBUF = 3;                  // K loads run two tiles ahead
+  static constexpr int LDS_BYTES = NBUF * 2 * TBUF * 2;
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -146,45 +150,77 @@ struct Bf16Pass {
 };
 
 // Fixed per-thread byte offsets of the direct loads of a tile: load i of wave w
-// fills LDS chunk P = (NW*i + w)*64 + lane, i.e. row P / RS, column P % RS.  Pad
-// columns and chunks past the tile's rows get an offset past any window, so they
-// read as zeros without touching memory.
+// of a group fills LDS chunk P = (4i + w)*64 + lane, i.e. row P / RS, column
+// P % RS.  Pad columns and chunks past the tile's rows get an offset past any
+// window, so they read as zeros without touching memory.
 template <int E, int RS, int NL>
-__device__ __forceinline__ void tile_offsets(int wv, int lane, int stride, int (&off)[NL]) {
-  constexpr int CPR = E / 8, BN = FlashBf16Cfg<E>::BN, NW = FlashBf16Cfg<E>::NW;
+__device__ __forceinline__ void tile_offsets(int wv4, int lane, int stride, int (&off)[NL]) {
+  constexpr int CPR = E / 8, BN = FlashBf16Cfg<E>::BN, NWG = FlashBf16Cfg<E>::NWG;
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
-    const int P = (NW * i + wv) * 64 + lane, r = P / RS, col = P % RS;
+    const int P = (NWG * i + wv4) * 64 + lane, r = P / RS, col = P % RS;
     off[i] = (r < BN && col < CPR) ? (r * stride + 8 * col) * 2 : (int)0x80000000;
   }
 }
 
-// Fills one K or V tile buffer: rows [k0, k0 + BN) of the source, cut at the
-// pass's key range (rows past it read as zeros, a tile past it touches no memory).
+// One wave's share of the successive K tiles (group 0) or V tiles (group 1) of
+// a pass: rows [k0, k0 + BN) of the source per tile, cut at the pass's key
+// range (rows past it read as zeros, a tile past it touches no memory), into
+// `nbuf` rotating tile buffers.  Every field is wave-uniform and advances by an
+// add per tile, so a tile's loads cost a few scalar instructions.
 // The loads are issued from inline assembly: the compiler does not track them,
 // so it inserts no wait for them before unrelated LDS reads (it cannot tell the
-// buffers apart); loads_done_barrier() waits for them explicitly.
+// buffers apart); loads_landed_barrier() waits for them explicitly.
 typedef __attribute__((ext_vector_type(4))) int i32x4;
-template <int E, int RS, int NL>
-__device__ __forceinline__ void fill_tile(uint16_t* buf, const uint16_t* src, int stride, int k0, int kend, int wv,
-                                          const int (&off)[NL]) {
-  constexpr int NW = FlashBf16Cfg<E>::NW;
-  const uint64_t addr = reinterpret_cast<uint64_t>(src + (int64_t)k0 * stride);
-  int64_t bytes = ((int64_t)(kend - 1 - k0) * stride + E) * 2;
-  bytes = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
-  // (wave-uniform values; readfirstlane keeps them in scalar registers even
-  // where the compiler cannot prove uniformity)
-  const i32x4 rs = {__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
-                    __builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffff)),
-                    __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
-  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>((lds_void*)buf));
+template <int E>
+struct TileStream {
+  static constexpr int BN = FlashBf16Cfg<E>::BN, NL = FlashBf16Cfg<E>::NL, NWG = FlashBf16Cfg<E>::NWG;
+  static constexpr uint32_t BUF_BYTES = FlashBf16Cfg<E>::TBUF * 2;
+  uint64_t addr;   // first row of the next tile
+  uint32_t step;   // bytes from one tile's first row to the next (< 2^31: the launcher checks)
+  int rows;        // rows of the key range from the next tile's first row on
+  int stride2;     // row stride in bytes
+  uint32_t lds;    // this wave's LDS byte address in the next tile's buffer
+  uint32_t lds0, lds_last;
+
+  __device__ __forceinline__ void init(const uint16_t* src, int stride, int kend, const uint16_t* buf0, int nbuf,
+                                       int first, int wv4) {
+    addr = reinterpret_cast<uint64_t>(src);
+    stride2 = 2 * stride;
+    step = (uint32_t)(BN * stride2);
+    rows = kend;
+    lds0 = (uint32_t)reinterpret_cast<uintptr_t>((const lds_void*)buf0) + wv4 * 1024;
+    lds_last = lds0 + (nbuf - 1) * BUF_BYTES;
+    lds = lds0 + first * BUF_BYTES;
+  }
+
+  // Loads of one tile through a window of `bytes` from `addr` (0: all zeros).
+  __device__ __forceinline__ void issue_window(int bytes, const int (&off)[NL]) {
+    const i32x4 rs = {__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
+                      __builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffff)),
+                      __builtin_amdgcn_readfirstlane(bytes), 0x00020000};
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
 #pragma unroll
-  for (int i = 0; i < NL; ++i)
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds + (NW * i + wv) * 1024), "v"(off[i]), "s"(rs)
-                 : "memory");
-}
+    for (int i = 0; i < NL; ++i)
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                   :
+                   : "s"(base + i * NWG * 1024), "v"(off[i]), "s"(rs)
+                   : "memory");
+    lds = lds == lds_last ? lds0 : lds + BUF_BYTES;
+  }
+
+  // The next tile of the key range.  A window of 2^31 - 1 bytes covers any tile
+  // (the launcher bounds BN rows of the stride below 2^31 bytes).
+  __device__ __forceinline__ void issue(const int (&off)[NL]) {
+    const int bytes = rows >= BN ? 0x7fffffff : (rows <= 0 ? 0 : (rows - 1) * stride2 + E * 2);
+    issue_window(bytes, off);
+    addr += step;
+    rows -= BN;
+  }
+
+  // A tile of zeros (no memory touched); the stream's position does not move.
+  __device__ __forceinline__ void issue_zeros(const int (&off)[NL]) { issue_window(0, off); }
+};
 
 // Waits until at most N of this wave's memory loads are outstanding (loads
 // complete in issue order), then the block barrier.
@@ -282,13 +318,12 @@ struct Bf16Rows {
 
   // p = 2^(s*c - m), rounded to bf16 for P.V as the reference's bf16 policy does
   // (flash_vec.mojo:255-259; l sums the unrounded p).  The 8 probabilities a lane
-  // holds per 16 keys are exactly the B operand of the P.V MFMA.  Returns the
-  // largest p as bits (positive floats order as integers).
+  // holds per 16 keys are exactly the B operand of the P.V MFMA.  Returns this
+  // lane's sum of p over the tile (it bounds every p of the lane).
   template <bool MASK>
-  __device__ __forceinline__ uint32_t softmax(const f32x16 (&st)[2], int vis, float c, bf16x8 (&pb)[4]) {
+  __device__ __forceinline__ float softmax(const f32x16 (&st)[2], int vis, float c, bf16x8 (&pb)[4]) {
     const float nmu = m == -INFINITY ? 0.f : -m;
     float ls = 0.f;
-    uint32_t pmax = 0;
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
       uint32_t w[4];
@@ -302,14 +337,13 @@ struct Bf16Rows {
         }
         const float e0 = __builtin_amdgcn_exp2f(fmaf(v0, c, nmu));
         const float e1 = __builtin_amdgcn_exp2f(fmaf(v1, c, nmu));
-        pmax = max(pmax, max(__float_as_uint(e0), __float_as_uint(e1)));
         ls += e0 + e1;
         w[jj / 2] = pack_bf16x2(e0, e1);
       }
       pb[cc] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
     }
     l += ls;
-    return pmax;
+    return ls;
   }
 
   // O^T += V^T P^T.
@@ -326,11 +360,14 @@ struct Bf16Rows {
   // as one stream of MFMAs whose LDS operand reads run LA operands ahead, in
   // scheduling regions of 4 MFMAs.  The lookahead keeps the LDS latency off the
   // MFMA pipe; the regions keep the compiler from hoisting every read (which
-  // would not fit in a wave's 256 registers).
-  template <bool PV, bool S>
+  // would not fit in a wave's 256 registers).  `mid` runs after the first
+  // region (the wave's tile loads, issued while its first MFMAs execute).
+  template <bool PV, bool S, typename F>
   __device__ __forceinline__ void mfma_phase(const uint16_t* vb, const bf16x8 (&pb)[4], const uint16_t* kb,
-                                             f32x16 (&st)[2]) {
+                                             f32x16 (&st)[2], F&& mid) {
     constexpr int NPV = PV ? 4 * ND : 0, NOP = NPV + (S ? 2 * NS : 0), LA = 8, R = LA + 1;
+    mid();
+    __builtin_amdgcn_sched_barrier(0);
     bf16x8 buf[R];
     auto read = [&](int i) {
       if (i < NPV) return v_operand<E>(vb, lane, i / ND, i % ND);
@@ -384,17 +421,26 @@ __device__ __noinline__ void bf16_safe_pass(const Bf16Pass& a, bool active) {
   constexpr int BN = C::BN, ND = E / 32;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   uint16_t* Ks = smem;
-  uint16_t* Vs = smem + C::NBUF * C::KBUF;
+  uint16_t* Vs = smem + C::NBUF * C::TBUF;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wg = wv >> 2, wv4 = wv & 3;
   Bf16Rows<E> w;
   w.lane = lane;
   w.li = lane & 31;
   w.hf = lane >> 5;
   w.r0 = a.q0 + 32 * wv;
-  int koff[C::NLK], voff[C::NLV];
-  tile_offsets<E, C::RSK>(wv, lane, a.ks1, koff);
-  tile_offsets<E, C::RSV>(wv, lane, a.vs1, voff);
+  // Group 0 loads the K tiles, group 1 the V tiles, each into one buffer.
+  int off[C::NL];
+  {
+    int koff[C::NL], voff[C::NL];
+    tile_offsets<E, C::RSK>(wv4, lane, a.ks1, koff);
+    tile_offsets<E, C::RSV>(wv4, lane, a.vs1, voff);
+#pragma unroll
+    for (int i = 0; i < C::NL; ++i) off[i] = wg ? voff[i] : koff[i];
+  }
+  TileStream<E> ts;
+  ts.init(wg ? a.v : a.k, wg ? a.vs1 : a.ks1, a.kend, wg ? Vs : Ks, 1, 0, wv4);
   const int nkt = a.kend > 0 ? (a.kend + BN - 1) / BN : 0;
   const int kend_w = a.causal ? min(a.S, w.r0 + 32 + a.diag) : a.S;
   const int nkt_w = active && kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
@@ -402,8 +448,7 @@ __device__ __noinline__ void bf16_safe_pass(const Bf16Pass& a, bool active) {
 
   __syncthreads();  // the fast walk is done with the tile buffers
   for (int t = 0; t < nkt; ++t) {
-    fill_tile<E, C::RSK>(Ks, a.k, a.ks1, t * BN, a.kend, wv, koff);
-    fill_tile<E, C::RSV>(Vs, a.v, a.vs1, t * BN, a.kend, wv, voff);
+    ts.issue(off);
     loads_done_barrier();
     if (t < nkt_w) {
       f32x16 st[2];
@@ -431,11 +476,11 @@ template <int E>
 __global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
   using C = FlashBf16Cfg<E>;
   constexpr int BM = C::BM, BN = C::BN;
-  // Headroom of the fast walk's fixed max: p <= 2^20 (a NaN p also exceeds it).
-  constexpr uint32_t kHeadBits = 0x49800000u;
+  // Headroom of the fast walk's fixed max: a lane's p summed over a tile <= 2^20.
+  constexpr float kHeadSum = 1048576.f;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* Ks = smem;                      // Kbuf[NBUF]
-  uint16_t* Vs = smem + C::NBUF * C::KBUF;  // Vbuf[NBUF]
+  uint16_t* Ks = smem;                      // K tile buffers [NBUF]
+  uint16_t* Vs = smem + C::NBUF * C::TBUF;  // V tile buffers [NBUF]
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches and windows
@@ -456,9 +501,17 @@ __global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
   a.v = reinterpret_cast<const uint16_t*>(p.v) + pw.b * p.vs[0] + pw.h * p.vs[2];
   a.out = reinterpret_cast<uint16_t*>(p.out) + (pw.b * p.seq_q * p.heads + pw.h) * E;
   const int S = a.S, diag = a.diag;
-  int koff[C::NLK], voff[C::NLV];
-  tile_offsets<E, C::RSK>(wv, lane, a.ks1, koff);
-  tile_offsets<E, C::RSV>(wv, lane, a.vs1, voff);
+  // Ping-pong groups: waves 0-3 and 4-7.  Group 0 loads the K tiles, group 1
+  // the V tiles.
+  const int wg = wv >> 2, wv4 = wv & 3;
+  int off[C::NL];
+  {
+    int koff[C::NL], voff[C::NL];
+    tile_offsets<E, C::RSK>(wv4, lane, a.ks1, koff);
+    tile_offsets<E, C::RSV>(wv4, lane, a.vs1, voff);
+#pragma unroll
+    for (int i = 0; i < C::NL; ++i) off[i] = wg ? voff[i] : koff[i];
+  }
 
   Bf16Rows<E> w;
   w.lane = lane;
@@ -481,59 +534,65 @@ __global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
 
     // The fast walk.  The row max is fixed at tile 0's (every row that sees any
     // key sees key 0) and never refreshed, so the loop touches the accumulators
-    // only through MFMAs; p stays below 2^20 unless a later logit exceeds the
-    // fixed max by more than 20 (log2 units), which `bad` records.
+    // only through MFMAs; the sum of a lane's p over a tile stays below 2^20
+    // (so every p does) unless a later logit exceeds the fixed max by about 20
+    // (log2 units) or more, which `bad` records.
     //
-    // Ping-pong: waves 0-3 (group 0) and 4-7 (group 1) share each SIMD and take
-    // turns, half a tile apart, between an MFMA phase (the S MFMAs of tile t and
-    // the P.V MFMAs of tile t-1) and a VALU phase (the softmax of tile t); a
-    // block barrier ends every half-step h.  Group g runs its MFMA phase for
-    // tile t at h = 2t + g and its softmax of tile t at h = 2t + g + 1, so K(t)
-    // is read at h = 2t, 2t+1 and V(t) at h = 2t+2, 2t+3.  Loads run two tiles
-    // ahead in three buffers: at even h = 2t every wave issues its share of the
-    // loads of K(t+2) and V(t+1) (into the buffers of K(t-1) and V(t-2), last
-    // read at h = 2t-1), and the barrier that ends h = 2t+1 waits for the loads
-    // issued at h = 2t-2 (K(t+1) and V(t)).
+    // Ping-pong: group 0 and group 1 share each SIMD and take turns, half a
+    // tile apart, between an MFMA phase (the S MFMAs of tile t and the P.V
+    // MFMAs of tile t-1) and a VALU phase (the softmax of tile t); a block
+    // barrier ends every half-step h.  Group g runs its MFMA phase for tile t at
+    // h = 2t + g and its softmax of tile t at h = 2t + g + 1, so K(t) is read at
+    // h = 2t, 2t+1 and V(t) at h = 2t+2, 2t+3.  Each MFMA phase issues the next
+    // tile of its group's stream: group 0 K(t+2) at h = 2t (into the buffer of
+    // K(t-1), last read at h = 2t-1), group 1 V(t+1) at h = 2t+1 (into the
+    // buffer of V(t-2), last read at h = 2t-1).  The barrier that ends an odd h
+    // = 2t+1 first waits for all but each wave's latest tile: K(t+1) and V(t),
+    // read from h = 2t+2 on.
     if (nkt > 0) {
-      constexpr int NL = C::NLK + C::NLV;  // direct loads per wave and tile
-      const int wg = wv >> 2;
+      constexpr int NL = C::NL;  // direct loads per wave and tile
       f32x16 st[2];
       bf16x8 pb[4];
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) pb[cc] = bf16x8{};
-      auto kbuf = [&](int t) { return Ks + (t % C::NBUF) * C::KBUF; };
-      auto vbuf = [&](int t) { return Vs + ((t + C::NBUF) % C::NBUF) * C::VBUF; };
-      fill_tile<E, C::RSK>(kbuf(0), a.k, a.ks1, 0, kend_b, wv, koff);
-      fill_tile<E, C::RSK>(kbuf(1), a.k, a.ks1, BN, kend_b, wv, koff);
-      fill_tile<E, C::RSV>(vbuf(0), a.v, a.vs1, 0, kend_b, wv, voff);
-      fill_tile<E, C::RSV>(vbuf(-1), a.v, a.vs1, 0, 0, wv, voff);  // zeros: an empty window
+      auto kbuf = [&](int t) { return Ks + (t % C::NBUF) * C::TBUF; };
+      auto vbuf = [&](int t) { return Vs + ((t + C::NBUF) % C::NBUF) * C::TBUF; };
+      TileStream<E> ts;
+      // K(j) goes to buffer j % 3; V(-1) (zeros: the P.V at t = 0 has p = 0,
+      // and 0 * a stale NaN would not be 0) to buffer 2, V(j) to buffer j % 3.
+      ts.init(wg ? a.v : a.k, wg ? a.vs1 : a.ks1, kend_b, wg ? Vs : Ks, C::NBUF, wg ? 2 : 0, wv4);
+      if (wg)
+        ts.issue_zeros(off);
+      else
+        ts.issue(off);
+      ts.issue(off);
       loads_done_barrier();
+      auto next_tile = [&] { ts.issue(off); };
       for (int h = 0; h < 2 * nkt + 2; ++h) {
-        if ((h & 1) == 0) {
-          const int t = h >> 1;
-          fill_tile<E, C::RSK>(kbuf(t + 2), a.k, a.ks1, (t + 2) * BN, kend_b, wv, koff);
-          fill_tile<E, C::RSV>(vbuf(t + 1), a.v, a.vs1, (t + 1) * BN, kend_b, wv, voff);
-        }
         if (((h + wg) & 1) == 0) {
           const int t = (h - wg) >> 1;
-          // Phases at t = 0 (P.V with pb = 0 over a zero-filled V buffer) and
+          // Phases at t = 0 (P.V with pb = 0 over the zero V buffer) and
           // t = nkt_w (S of a tile it does not use) run the same code.
           if (t <= nkt_w && nkt_w > 0) {
             __builtin_amdgcn_s_setprio(1);
-            w.template mfma_phase<true, true>(vbuf(t - 1), pb, kbuf(t), st);
+            w.template mfma_phase<true, true>(vbuf(t - 1), pb, kbuf(t), st, next_tile);
             __builtin_amdgcn_s_setprio(0);
+          } else {
+            next_tile();
           }
         } else {
           const int t = (h - 1 - wg) >> 1;
           if (t >= 0 && t < nkt_w) {
             const int k0 = t * BN;
+            float ls;
             if (t == 0 || k0 + BN > S || (p.causal && k0 + BN - 1 > w.r0 + diag)) {
               const int vis = w.vis_of(a, t);
               if (t == 0) w.m = w.tile_max(st, vis, a.c);
-              bad |= w.template softmax<true>(st, vis, a.c, pb) > kHeadBits;
+              ls = w.template softmax<true>(st, vis, a.c, pb);
             } else {
-              bad |= w.template softmax<false>(st, BN, a.c, pb) > kHeadBits;
+              ls = w.template softmax<false>(st, BN, a.c, pb);
             }
+            bad |= !(ls <= kHeadSum);  // also NaN
           }
         }
         if (h & 1)
