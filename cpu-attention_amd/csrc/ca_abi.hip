@@ -141,9 +141,11 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
   return decode_launch(p, (int)a->head_dim, a->dtype == CA_BF16, st);
 }
 
-extern "C" int64_t ca_flash_workspace_bytes(int64_t, int64_t, int64_t, int64_t, int64_t,
-                                            int32_t) {
-  return 0;
+extern "C" int64_t ca_flash_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t num_heads,
+                                            int64_t head_dim, int32_t dtype) {
+  if (!dtype_ok(dtype) || !head_dim_ok(head_dim) || batch < 0 || num_heads < 0 || seq_q < 1 || seq_k < 1)
+    return 0;
+  return flash_rows_workspace_bytes(batch, seq_q, seq_k, num_heads, (int)head_dim, dtype == CA_BF16);
 }
 
 extern "C" int ca_flash(const ca_flash_args* a, void* stream) {
@@ -173,5 +175,7 @@ extern "C" int ca_flash(const ca_flash_args* a, void* stream) {
   }
   p.c = a->scale * kLog2e;
   p.causal = a->causal ? 1 : 0;
+  if (a->workspace_bytes < 0) return CA_DECLINED;
+  flash_rows_workspace(p, a->workspace, a->workspace_bytes, (int)a->head_dim, a->dtype == CA_BF16);
   return flash_launch(p, (int)a->head_dim, a->dtype == CA_BF16, static_cast<hipStream_t>(stream));
 }

@@ -41,15 +41,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
 }
 
-// Hardware dispatches workgroup i to XCD i % 8.  Remap so each XCD walks a
-// contiguous range of (batch*head, query block) work: one head's K/V stays in
-// that XCD's L2 while its query blocks run.
-__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nb) {
-  const int64_t x = bid & 7, slot = bid >> 3;
-  const int64_t per = nb >> 3, rem = nb & 7;
-  return x * per + (x < rem ? x : rem) + slot;
-}
-
 struct BlockWork {
   int64_t b, h, q0;
 };
@@ -801,6 +792,7 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
     return CA_DECLINED;
   // Row and key positions are 32-bit inside the kernels.
   if (p.seq_q >= ((int64_t)1 << 30) || p.seq_k >= ((int64_t)1 << 30)) return CA_DECLINED;
+  if (rows_route(p.seq_q, bf16 != 0)) return flash_rows_launch(p, E, bf16, stream);
   if (bf16) {
     // One block per (batch, head) and query-block pair (causal) or query block.
     const int64_t nqb = cdiv(p.seq_q, FlashBf16Cfg<128>::BM);

@@ -48,12 +48,30 @@ struct FlashParams {
   int64_t qs[3], ks[3], vs[3];  // batch, token, head strides (elements)
   float c;                      // softmax scale * log2(e)
   int causal;
+  // Few-rows route only: split-K partials in the caller's workspace.
+  float* part_acc;              // [batch*heads*seq_q, splits, E]
+  float* part_ml;               // [batch*heads*seq_q, splits, 2]: max (scaled log2 units), sum
+  int64_t workspace_bytes;
 };
+
+// Calls with few query rows take the few-rows route (ca_rows.hip): up to 4 rows
+// in bf16 (past that the tiled MFMA kernel is faster on MI355X), up to 16 in
+// fp32; kRowsPerWave rows per wave.
+constexpr int64_t kRowsMaxL = 16;
+constexpr int kRowsPerWave = 4;
+__host__ __device__ inline bool rows_route(int64_t seq_q, bool bf16) { return seq_q <= (bf16 ? 4 : kRowsMaxL); }
+constexpr int kRowsWaves = 8;                 // waves per block
+constexpr int64_t kRowsTargetBlocks = 256;    // blocks that keep every CU streaming
+constexpr int64_t kRowsMaxSplits = 64;
 
 int store_launch(const StoreParams& p, int words, hipStream_t stream);
 int64_t decode_tiles(int64_t pt_width, int64_t page);
 int64_t decode_workspace_slots(int64_t rows, int64_t tiles);
 int decode_launch(const DecodeParams& p, int head_dim, int bf16, hipStream_t stream);
 int flash_launch(const FlashParams& p, int head_dim, int bf16, hipStream_t stream);
+int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, int head_dim,
+                                   bool bf16);
+void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int head_dim, bool bf16);
+int flash_rows_launch(const FlashParams& p, int head_dim, int bf16, hipStream_t stream);
 
 }  // namespace ca

@@ -98,6 +98,36 @@ def test_entries_decline_malformed_calls_without_a_gpu():
     assert lib.ca_flash_workspace_bytes(1, 1, 1, 1, 64, 1) == 0
 
 
+@pytest.mark.parametrize("dtype,d,chunk", [(1, 32, 64), (1, 64, 32), (1, 128, 16),
+                                           (0, 32, 32), (0, 64, 16), (0, 128, 8)])
+def test_flash_workspace_for_few_rows(dtype, d, chunk):
+    """Few query rows (up to 4 in bf16, 16 in fp32) go to blocks of 8 waves per
+    (batch, head, row group: 1 row for single-row calls, else 4); chunks of 4 load
+    steps (16-byte slices, 64 lanes).  Only when those blocks number fewer than 256
+    are a row group's chunks split over more blocks (at most one chunk per wave and
+    64 splits), which needs (E + 2) floats per (batch, head, row, split);
+    otherwise no workspace."""
+    lib = K.load_library()
+
+    def expect(b, sq, sk, h):
+        if sq > (4 if dtype == 1 else 16):
+            return 0
+        blocks = b * h * -(-sq // (1 if sq == 1 else 4))
+        splits = 1 if blocks >= 256 else -(-256 // blocks)
+        splits = max(1, min(splits, -(-(-(-sk // chunk)) // 8), 64))
+        return 0 if splits == 1 else b * h * sq * splits * (d + 2) * 4
+
+    for b, sq, sk, h in ((1, 1, 100000, 1), (2, 16, 1000, 3), (3, 4, chunk + 1, 5), (8, 1, 2048, 32),
+                         (1, 3, 70000, 2)):
+        assert lib.ca_flash_workspace_bytes(b, sq, sk, h, d, dtype) == expect(b, sq, sk, h)
+    assert lib.ca_flash_workspace_bytes(1, 1, 100000, 1, d, dtype) == 1 * 1 * 1 * 64 * (d + 2) * 4
+    assert lib.ca_flash_workspace_bytes(8, 1, 2048, 32, d, dtype) == 0  # 256 blocks fill the chip
+    assert lib.ca_flash_workspace_bytes(3, 4, 8 * chunk, 5, d, dtype) == 0  # one chunk per wave
+    assert lib.ca_flash_workspace_bytes(3, 17, 5000, 5, d, dtype) == 0  # the tiled route
+    assert (lib.ca_flash_workspace_bytes(1, 5, 50000, 1, d, dtype) == 0) == (dtype == 1)  # bf16: tiled
+    assert lib.ca_flash_workspace_bytes(3, 4, 5000, 5, 48, dtype) == 0  # head_dim
+
+
 def test_missing_library_is_a_loud_error(monkeypatch):
     monkeypatch.setenv("CPU_ATTENTION_LIB", "/nonexistent/libcpu_attention_hip.so")
     monkeypatch.setattr(K, "_MODULE", None)

@@ -1,0 +1,109 @@
+"""flash_attn_func calls with few query rows (up to 4 in bf16, 16 in fp32), which
+take the split-K few-rows route, against the float64 oracle.  Covers every head
+dim and dtype, key lengths at and past the chunk edges (one chunk, several, a
+partial last one), single rows and row groups of 4 with a partial last group,
+causal rows that see no key, strided q/k/v views, the boundary with the tiled
+route, the cross shape of the BASELINE prefill config, and the workspace
+protocol (the first call of a thread finds the workspace short and retries)."""
+
+import threading
+
+import numpy as np
+import pytest
+import torch
+
+from cpu_attention import _kernel as K
+from cpu_attention import flash_attn_func
+from helpers import assert_close, attention, values
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+def run(b, sq, sk, h, d, dtype, causal, seed, device, scale=None):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(b, n, h, d, generator=g).to(dtype).to(device) for n in (sq, sk, sk))
+    out = flash_attn_func(q, k, v, softmax_scale=scale, causal=causal)
+    assert out.shape == q.shape and out.dtype == dtype and out.is_contiguous()
+    ref = attention(values(q), values(k), values(v), scale or d ** -0.5, causal)
+    assert_close(out, ref, dtype, paged=False)
+    return out
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("sq", [1, 2, 3, 4, 5, 16])
+@pytest.mark.parametrize("sk", [1, 31, 32, 33, 128, 129, 300, 1100])
+@pytest.mark.parametrize("causal", [True, False])
+def test_few_rows_shapes(cuda, dtype, d, sq, sk, causal):
+    run(2, sq, sk, 3, d, dtype, causal, seed=sq * 10000 + sk * 10 + d, device=cuda)
+
+
+@pytest.mark.parametrize("dtype,sq", [(torch.bfloat16, 4), (torch.bfloat16, 5),
+                                      (torch.float32, 16), (torch.float32, 17)])
+def test_route_boundary(cuda, dtype, sq):
+    """The last row count of the few-rows route and the first of the tiled one
+    both agree with the oracle."""
+    run(2, sq, 700, 4, 64, dtype, True, seed=sq, device=cuda)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_causal_rows_without_keys(cuda, dtype):
+    """seq_q > seq_k: the first seq_q - seq_k rows see no key and are exactly 0."""
+    out = run(1, 16, 5, 2, 64, dtype, True, seed=3, device=cuda)
+    assert torch.count_nonzero(out[:, :11]) == 0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_strided_views(cuda, dtype):
+    """q/k/v as chunks of a fused projection (token stride 3*H*E), with a batch
+    stride that is not a multiple of the token stride."""
+    b, sq, sk, h, d = 3, 3, 500, 4, 32
+    g = torch.Generator().manual_seed(5)
+    kv = torch.randn(b, sk + 7, 3 * h * d, generator=g).to(dtype).to(cuda)[:, :sk]
+    k, v = (kv[..., i * h * d:(i + 1) * h * d].view(b, sk, h, d) for i in (0, 2))
+    q = torch.randn(b, sq, h, d, generator=g).to(dtype).to(cuda)
+    out = flash_attn_func(q, k, v, causal=False)
+    assert_close(out, attention(values(q), values(k), values(v), d ** -0.5), dtype, paged=False)
+
+
+def test_scale_and_large_logits(cuda):
+    """A large scale (logits spread over many chunks' maxima) in fp32."""
+    run(2, 4, 2000, 2, 128, torch.float32, False, seed=9, device=cuda, scale=0.5)
+
+
+def test_cfg4_cross_shape_rows(cuda):
+    """BASELINE config 3's cross shape: N=8 L=1 S=2048 E=32 H=32, non-causal, bf16."""
+    run(8, 1, 2048, 32, 32, torch.bfloat16, False, seed=12, device=cuda)
+
+
+def test_workspace_grows_in_a_new_thread(cuda):
+    """A fresh thread has no workspace: the first call finds it short, grows it
+    and retries (the reference's flash_attn_interface.py:186-193 protocol)."""
+    errs = []
+
+    def work():
+        try:
+            assert K.workspace() == (0, 0)
+            run(2, 2, 3000, 8, 64, torch.bfloat16, False, seed=21, device=cuda)
+            assert K.workspace()[1] > 0
+        except Exception as e:  # noqa: BLE001 - reported below
+            errs.append(e)
+
+    t = threading.Thread(target=work)
+    t.start()
+    t.join()
+    assert not errs, errs
+
+
+def test_native_entry_reports_the_workspace_it_needs(cuda):
+    """The module entry returns the bytes it needs (an int) when the workspace is short."""
+    mod, rt = K.module(), K.runtime()
+    q = torch.randn(1, 1, 4, 64, device=cuda)
+    k = torch.randn(1, 4000, 4, 64, device=cuda)
+    need = mod.flash(rt, q, k, k, None, False, 0, 0)
+    assert type(need) is int and need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=cuda)
+    out = mod.flash(rt, q, k, k, None, False, ws.data_ptr(), need)
+    ref = attention(values(q), values(k), values(k), 64 ** -0.5)
+    assert np.abs(values(out) - ref).max() <= 1e-5
