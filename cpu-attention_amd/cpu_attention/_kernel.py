@@ -32,7 +32,7 @@ DTYPES = {torch.float32: 0, torch.bfloat16: 1}
 HEAD_DIMS = (32, 64, 128)
 _DIR = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = "libcpu_attention_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 _ESIZE = {torch.float32: 4, torch.bfloat16: 2}
 _PLAIN = (torch.Tensor, torch.nn.Parameter)
 
@@ -63,6 +63,7 @@ class DecodeArgs(ctypes.Structure):
         ("head_dim", ctypes.c_int64), ("page_size", ctypes.c_int64),
         ("num_blocks", ctypes.c_int64), ("scale", ctypes.c_float), ("dtype", ctypes.c_int32),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+        ("new_tokens", ctypes.c_int64),
     ]
 
 
@@ -206,6 +207,32 @@ class Module:
         ``lens`` is the length after the store), or appended at ``lens`` (the
         length before). Writes ``dst`` when given, else a new tensor; returns it,
         or None for anything the kernels do not take."""
+        return self._decode(q, k_cache, v_cache, k, v, slots, lens, page_table, scale, dst, 1)
+
+    def append_decode(self, rt, q, k_cache, v_cache, k, v, lens, page_table, scale):
+        """The prompt append of flash_attn_with_kvcache (flash_attn_interface.py:109-117)
+        in one native call: token j of ``k``/``v`` ``[seqs, n, heads, dim]`` is stored
+        at position ``lens + j`` of its sequence (through the page table, inside
+        the store kernel), then q attends ``lens + n`` keys. Returns the output, or
+        None for anything the kernels do not take (the caller then takes the
+        reference's path, which raises the precise error)."""
+        if not (isinstance(k, torch.Tensor) and isinstance(v, torch.Tensor)):
+            return None
+        if not (_plain(k) and _plain(v)) or k.dim() != 4 or v.shape != k.shape \
+                or not isinstance(q, torch.Tensor) or q.shape[0] != k.shape[0] \
+                or tuple(k.shape[2:]) != tuple(q.shape[-2:]):
+            return None
+        b, n = k.shape[0], k.shape[1]
+        if n < 1:
+            return None
+        kr, vr = k.reshape(b * n, *k.shape[2:]), v.reshape(b * n, *v.shape[2:])
+        if vr.stride() != kr.stride():
+            return None
+        return self._decode(q, k_cache, v_cache, kr, vr, None, lens, page_table, scale, None, n)
+
+    def _decode(self, q, k_cache, v_cache, k, v, slots, lens, page_table, scale, dst, n):
+        """decode() with ``n`` new tokens per sequence (k/v rows ``[seqs * n, heads,
+        dim]`` when n > 1, appended at ``lens``)."""
         if not (_plain(q) and _plain(page_table) and isinstance(lens, torch.Tensor)):
             return None
         nd = q.dim()
@@ -225,7 +252,8 @@ class Module:
             return None
         store = k is not None
         if store:
-            if not (_plain(k) and _plain(v) and k.shape == q.shape and v.shape == q.shape
+            rows = q.shape if n == 1 else (b * n, heads, hd)
+            if not (_plain(k) and _plain(v) and k.shape == rows and v.shape == rows
                     and v.stride() == k.stride()):
                 return None
             if k.dtype != q.dtype or v.dtype != q.dtype or not _rows_ok(k, hd):
@@ -251,7 +279,7 @@ class Module:
         if _HOST_CHECKS[0] and b:
             if slots is not None and int(slots.max()) >= nblocks * page:
                 return None
-            if int(lens.max()) + (1 if store and slots is None else 0) > width * page:
+            if int(lens.max()) + (n if store and slots is None else 0) > width * page:
                 return None
         lens = _index_on(lens, dev)
         page_table = _index_on(page_table, dev)
@@ -268,7 +296,7 @@ class Module:
             page_table=page_table.data_ptr(), page_table_width=width, out=out.data_ptr(),
             num_seqs=b, num_heads=heads, head_dim=hd, page_size=page, num_blocks=nblocks,
             scale=float(hd) ** -0.5 if scale is None else float(scale), dtype=DTYPES[q.dtype],
-            workspace=ws.data_ptr(), workspace_bytes=ws.numel())
+            workspace=ws.data_ptr(), workspace_bytes=ws.numel(), new_tokens=n if store else 0)
         rc = self.lib.ca_decode(ctypes.byref(args), _stream(dev))
         if rc == CA_DECLINED:
             return None

@@ -131,9 +131,16 @@ def flash_attn_with_kvcache(
         cache_seqlens = torch.full((q.shape[0],), cache_seqlens, dtype=torch.int32, device=dev)
     if k is not None and k.shape[1] != 1:
         # Several new tokens (a prompt): store them at cache_seqlens + j, then
-        # decode over the grown cache.  Positions outside the page table get slot
-        # -1 (not stored) instead of an out-of-range gather; the decode below then
-        # reports the overflow.
+        # decode over the grown cache.  One native call does both (the slots are
+        # computed in the store kernel); anything it does not take goes the
+        # reference's way below, which raises the precise error.
+        out = K.module().append_decode(K.runtime(), q, k_cache, v_cache, k, v, cache_seqlens,
+                                       page_table, softmax_scale) \
+            if isinstance(q, torch.Tensor) and isinstance(k, torch.Tensor) else None
+        if out is not None:
+            return out
+        # Positions outside the page table get slot -1 (not stored) instead of an
+        # out-of-range gather; the decode below then reports the overflow.
         n, page = k.shape[1], k_cache.shape[2]
         table = page_table.to(k.device).long()
         pos = cache_seqlens.to(k.device).long()[:, None] + torch.arange(n, device=k.device)[None]

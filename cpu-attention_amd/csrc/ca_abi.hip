@@ -25,7 +25,7 @@ bool page_ok(int64_t page) { return page > 0 && page % 16 == 0; }
 extern "C" int ca_abi_version(void) { return CA_ABI_VERSION; }
 
 extern "C" const char* ca_version(void) {
-  return "cpu-attention gfx950 (MI355X) HIP kernels, ABI " "1";
+  return "cpu-attention gfx950 (MI355X) HIP kernels, ABI " "2";
 }
 
 extern "C" const char* ca_status_string(int status) {
@@ -54,6 +54,7 @@ extern "C" int ca_store(const ca_store_args* a, void* stream) {
   p.vc = static_cast<uint32_t*>(a->v_cache);
   p.slots = a->slot_mapping;
   p.ntok = a->num_tokens;
+  p.per_seq = 1;
   p.heads = a->num_heads;
   p.page = a->page_size;
   p.nblocks = a->num_blocks;
@@ -85,6 +86,8 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
     return CA_DECLINED;
   if ((a->k_new == nullptr) != (a->v_new == nullptr)) return CA_DECLINED;
   if (a->slots && !a->k_new) return CA_DECLINED;
+  if (a->new_tokens < 0 || a->new_tokens > (1 << 30) || (a->slots && a->new_tokens > 1)) return CA_DECLINED;
+  const int64_t per_seq = a->new_tokens > 1 ? a->new_tokens : 1;
   if (!aligned16(a->q) || !aligned16(a->k_cache) || !aligned16(a->v_cache) ||
       !aligned16(a->out) || !stride16(a->q_stride, a->dtype))
     return CA_DECLINED;
@@ -108,7 +111,8 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
     sp.lens = a->lens;
     sp.page_table = a->page_table;
     sp.pt_width = a->page_table_width;
-    sp.ntok = a->num_seqs;
+    sp.ntok = a->num_seqs * per_seq;
+    sp.per_seq = per_seq;
     sp.heads = a->num_heads;
     sp.page = a->page_size;
     sp.nblocks = a->num_blocks;
@@ -124,7 +128,7 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
   p.lens = a->lens;
   // Appending at lens: the row attends lens + 1 keys.  With slots, lens is
   // already the post-store length (_C.mojo:100-103, paged_attn.mojo:721-723).
-  p.len_add = (a->k_new && !a->slots) ? 1 : 0;
+  p.len_add = (a->k_new && !a->slots) ? (int32_t)per_seq : 0;
   p.page_table = a->page_table;
   p.pt_width = a->page_table_width;
   p.heads = a->num_heads;

@@ -14,10 +14,11 @@ struct StoreParams {
   uint32_t* kc;           // per (block, head): W word rows of P tokens (K transposed)
   uint32_t* vc;           // per (block, head): P rows of W words
   const int64_t* slots;   // slot mode: [T]; nullptr selects append mode
-  const int32_t* lens;    // append mode: [T] positions (the pre-store lengths)
+  const int32_t* lens;    // append mode: [T / per_seq] positions (the pre-store lengths)
   const int32_t* page_table;
   int64_t pt_width;
   int64_t ntok, heads, page, nblocks;
+  int64_t per_seq;        // append mode: consecutive tokens per sequence
   int heads_per_block;
 };
 
@@ -27,7 +28,7 @@ struct DecodeParams {
   const uint32_t* kc;     // K cache as 32-bit words
   const void* vc;
   const int32_t* lens;
-  int32_t len_add;        // 1 when the row also attends a token appended at lens
+  int32_t len_add;        // tokens appended at lens that the row also attends
   const int32_t* page_table;
   int64_t pt_width;
   int64_t heads, page, nblocks, nseqs;

@@ -30,13 +30,16 @@ __device__ __forceinline__ void store_target(const StoreParams& p, int64_t i, in
       off = s - blk * p.page;
     }
   } else {
-    // Append at the pre-store length through the page table (paged_attn.mojo:165-170);
-    // a negative length stores nothing.
-    int64_t pos = p.lens[i];
-    if (pos >= 0) {
+    // Append at the pre-store length through the page table (paged_attn.mojo:165-170):
+    // token j of a sequence goes to position lens + j; a negative length stores
+    // nothing, nor does a position past the page table.
+    const int64_t seq = p.per_seq == 1 ? i : i / p.per_seq;
+    const int64_t len = p.lens[seq];
+    int64_t pos = len + (i - seq * p.per_seq);
+    if (len >= 0) {
       int64_t pi = pos / p.page;
       if (pi < p.pt_width) {
-        int64_t b = p.page_table[i * p.pt_width + pi];
+        int64_t b = p.page_table[seq * p.pt_width + pi];
         if (b >= 0 && b < p.nblocks) {
           blk = b;
           off = pos - pi * p.page;

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define CA_ABI_VERSION 1
+#define CA_ABI_VERSION 2
 
 enum { CA_F32 = 0, CA_BF16 = 1 };
 
@@ -77,16 +77,25 @@ int ca_store(const ca_store_args* args, void* stream);
  * cached K/V, online softmax in base 2, fp32 accumulation, output in the input
  * dtype; a row with no key is exactly 0.
  *
- * With k_new/v_new (one token per sequence) the token is stored first:
- *   slots == NULL: at position lens[s] through page_table (lens is the length
- *                  before the store; the row attends lens[s] + 1 keys;
- *                  lens[s] < 0 stores nothing);
- *   slots != NULL: at slot slots[s] (negative skips), and lens[s] is the
- *                  length after the store (the engine path, examples/ops.py:19-25).
+ * With k_new/v_new the new tokens are stored first:
+ *   slots == NULL: new_tokens tokens per sequence (0 counts as 1), token j of
+ *                  sequence s at position lens[s] + j through page_table (lens is
+ *                  the length before the store; the row attends lens[s] +
+ *                  new_tokens keys; lens[s] < 0 stores nothing, positions past
+ *                  the page table are not stored).  One token is the reference's
+ *                  append; several are its prompt append, which the reference
+ *                  builds from slot arithmetic and reshape_and_cache
+ *                  (flash_attn_interface.py:109-117) and this entry computes
+ *                  inside the store kernel;
+ *   slots != NULL: one token per sequence at slot slots[s] (negative skips), and
+ *                  lens[s] is the length after the store (the engine path,
+ *                  examples/ops.py:19-25); new_tokens must be 0 or 1.
  * Without k_new/v_new the row attends lens[s] keys.
  *
- * q, k_new, v_new: [num_seqs, num_heads, head_dim] rows, heads and dims
- * contiguous, sequence stride q_stride / kv_stride (elements).
+ * q: [num_seqs, num_heads, head_dim] rows, heads and dims contiguous, sequence
+ * stride q_stride (elements).  k_new, v_new: rows of [num_seqs * new_tokens,
+ * num_heads, head_dim] (token j of sequence s is row s * new_tokens + j), heads
+ * and dims contiguous, row stride kv_stride.
  * out: [num_seqs, num_heads, head_dim] contiguous.
  * workspace: at least ca_decode_workspace_bytes(...) bytes of device memory,
  * 256-byte aligned; its contents need not be initialised. */
@@ -112,6 +121,7 @@ typedef struct ca_decode_args {
   int32_t dtype;
   void* workspace;
   int64_t workspace_bytes;
+  int64_t new_tokens;  /* tokens per sequence in k_new/v_new (0 or 1: one) */
 } ca_decode_args;
 
 int64_t ca_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t head_dim,

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_entry():
 
 def test_version_and_status_strings():
     lib = K.load_library()
-    assert lib.ca_abi_version() == K.ABI_VERSION == 1
+    assert lib.ca_abi_version() == K.ABI_VERSION == 2
     assert b"gfx950" in lib.ca_version()
     assert lib.ca_status_string(0) == b"ok"
     assert b"declined" in lib.ca_status_string(1)

@@ -264,3 +264,89 @@ def test_many_sequences(cuda, nseqs):
             ref[i] = attention(qv[i:i + 1], kv[None, starts[i]:starts[i + 1]],
                                vv[None, starts[i]:starts[i + 1]], d ** -0.5)[0]
     assert_close(out, ref, torch.bfloat16, paged=True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [2, 40, 100])
+def test_prompt_append_in_one_call(cuda, dtype, n):
+    """The prompt append (k/v with n new tokens per sequence) through the single
+    native call: the cache bytes are what the layout oracle's prompt slots give,
+    and q attends every old and new token."""
+    lens, h, d, page = [0, 5, 31, 100], 4, 64, 16
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=n, device=cuda)
+    # Room for n more tokens: each sequence keeps its pages and gets fresh
+    # (NaN-filled) blocks for the rest of a wider page table.
+    cols = -(-(max(lens) + n) // page)
+    nb, table = kc.shape[0], bt.cpu()
+    rows = []
+    for i, m in enumerate(lens):
+        own = -(-m // page)
+        fresh = torch.arange(nb, nb + cols - own, dtype=torch.int32)
+        nb += cols - own
+        rows.append(torch.cat([table[i, :own], fresh]))
+    bt = torch.stack(rows).to(cuda)
+    pad = torch.full((nb - kc.shape[0], *kc.shape[1:]), float("nan"), dtype=dtype, device=cuda)
+    kc, vc = torch.cat([kc, pad]), torch.cat([vc, pad.clone()])
+    g = torch.Generator().manual_seed(100 + n)
+    kn, vn = (torch.randn(len(lens), n, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))
+    kw, vw = cache_words(kc), cache_words(vc)
+    for i in range(len(lens)):
+        s = layout.prompt_slots(lens[i], n, bt[i].cpu().numpy(), page)
+        layout.store(kw, vw, row_words(kn[i]), row_words(vn[i]), s, page)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    out = flash_attn_with_kvcache(q, kc, vc, k=kn, v=vn, cache_seqlens=seqlens, page_table=bt)
+    np.testing.assert_array_equal(cache_words(kc), kw)
+    np.testing.assert_array_equal(cache_words(vc), vw)
+    ks2 = [torch.cat([a, kn[i:i + 1]], 1) for i, a in enumerate(ks)]
+    vs2 = [torch.cat([a, vn[i:i + 1]], 1) for i, a in enumerate(vs)]
+    assert_close(out, reference(q, ks2, vs2, d ** -0.5), dtype, paged=True)
+    assert torch.equal(seqlens.cpu(), torch.tensor(lens, dtype=torch.int32))  # not mutated
+
+
+def test_prompt_append_strided_and_cpu_lengths(cuda):
+    """k/v as strided chunks of a fused projection and cache_seqlens as an int or
+    a CPU tensor take the same single call."""
+    h, d, page, n = 2, 32, 16, 20
+    nb = 8
+    table = torch.arange(nb, dtype=torch.int32).view(2, 4)
+    kc = torch.zeros(nb, h, page, d, dtype=torch.bfloat16, device=cuda)
+    vc = torch.zeros_like(kc)
+    g = torch.Generator().manual_seed(7)
+    kv = torch.randn(2, n, 3 * h * d, generator=g).bfloat16().to(cuda)
+    k, v = (kv[..., i * h * d:(i + 1) * h * d].view(2, n, h, d) for i in (0, 2))
+    q = torch.randn(2, 1, h, d, generator=g).bfloat16().to(cuda)
+    out = flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=0, page_table=table.to(cuda))
+    ref = reference(q, [k[0:1], k[1:2]], [v[0:1], v[1:2]], d ** -0.5)
+    assert_close(out, ref, torch.bfloat16, paged=True)
+    out2 = flash_attn_with_kvcache(q, kc, vc, cache_seqlens=torch.tensor([n, n], dtype=torch.int32),
+                                   page_table=table)
+    assert_close(out2, ref, torch.bfloat16, paged=True)
+
+
+def test_prompt_append_past_the_page_table(cuda):
+    """More new tokens than the page table holds: with host checks the reference's
+    ValueError; without them no fault, the tokens that fit are stored and the
+    row attends the table's capacity."""
+    h, d, page = 2, 64, 16
+    table = torch.tensor([[0, 1]], dtype=torch.int32, device=cuda)
+    kc = torch.zeros(2, h, page, d, device=cuda)
+    vc = torch.zeros_like(kc)
+    k = torch.randn(1, 40, h, d, device=cuda)
+    q = torch.randn(1, 1, h, d, device=cuda)
+    with pytest.raises(ValueError):
+        flash_attn_with_kvcache(q, kc, vc, k=k, v=k, cache_seqlens=torch.tensor([0], dtype=torch.int32,
+                                                                                device=cuda),
+                                page_table=table)
+    old = K.set_host_checks(False)
+    try:
+        kc.zero_()
+        vc.zero_()
+        out = K.module().append_decode(K.runtime(), q, kc, vc, k, k, torch.tensor([0], dtype=torch.int32,
+                                                                                   device=cuda), table, None)
+        assert out is not None and torch.isfinite(out).all()
+        assert torch.equal(vc[0].permute(1, 0, 2).reshape(-1, h, d), k[0, :16])
+        assert torch.equal(vc[1].permute(1, 0, 2).reshape(-1, h, d), k[0, 16:32])
+        ref = attention(values(q[0:1]), values(k[:, :32]), values(k[:, :32]), d ** -0.5)
+        assert np.abs(values(out) - ref).max() <= 1e-5
+    finally:
+        K.set_host_checks(old)
