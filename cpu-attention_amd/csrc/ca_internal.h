@@ -19,7 +19,6 @@ struct StoreParams {
   int64_t pt_width;
   int64_t ntok, heads, page, nblocks;
   int64_t per_seq;        // append mode: consecutive tokens per sequence
-  int heads_per_block;
 };
 
 struct DecodeParams {

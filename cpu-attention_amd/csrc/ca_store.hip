@@ -8,7 +8,9 @@
 // K is transposed inside the page (word (w, t) at w*P + t): a block stages 16
 // tokens' K rows in LDS and writes word w of the 16 tokens from 16 neighbouring
 // lanes, so tokens in consecutive slots of one page become one contiguous 64-byte
-// run per word row.  Bytes are moved, never converted: the result is bit-exact.
+// run per word row.  A block takes 16 tokens of 256/W heads (grid.y walks the
+// heads) and issues all of its loads before any store, so every CU keeps many
+// rows in flight.  Bytes are moved, never converted: the result is bit-exact.
 #include "ca_device.h"
 #include "ca_internal.h"
 
@@ -51,72 +53,89 @@ __device__ __forceinline__ void store_target(const StoreParams& p, int64_t i, in
 
 template <int W>
 __global__ __launch_bounds__(256) void store_kernel(StoreParams p) {
-  constexpr int LD = W + 1;  // padded LDS row: the transposed reads hit 16 distinct banks
-  constexpr int Q4 = W / 4;  // 16-byte chunks per row
-  __shared__ uint32_t kbuf[kStoreTok * LD];
+  constexpr int LD = W + 1;                          // padded LDS row: transposed reads hit distinct banks
+  constexpr int Q4 = W / 4;                          // 16-byte chunks per row
+  constexpr int HB = 256 / W;                        // heads per block
+  constexpr int NCH = kStoreTok * HB * Q4 / 256;     // chunks per thread (K and V each): 4
+  static_assert(NCH * 256 == kStoreTok * HB * Q4, "block shape");
+  __shared__ uint32_t kbuf[HB][kStoreTok * LD];
   __shared__ int64_t s_blk[kStoreTok];
   __shared__ int64_t s_off[kStoreTok];
 
   const int tid = threadIdx.x;
-  const int64_t i0 = (int64_t)blockIdx.x * kStoreTok;
+  // One-dimensional grid over (head group, token group), token groups fastest;
+  // neighbouring token groups share an XCD, so the two blocks that write parts
+  // of one page's 64-byte K word rows meet in one L2.
+  const int64_t ngx = cdiv(p.ntok, kStoreTok);
+  const int64_t lg = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t gy = lg / ngx;
+  const int64_t i0 = (lg - gy * ngx) * kStoreTok;
   const int nt = (int)min<int64_t>(kStoreTok, p.ntok - i0);
+  const int64_t h0 = gy * HB;
   if (tid < kStoreTok) {
     int64_t blk = -1, off = 0;
     if (tid < nt) store_target(p, i0 + tid, blk, off);
     s_blk[tid] = blk;
     s_off[tid] = off;
   }
-  __syncthreads();
-
-  const int64_t h0 = (int64_t)blockIdx.y * p.heads_per_block;
-  const int64_t h1 = min<int64_t>(p.heads, h0 + p.heads_per_block);
-  const int64_t page_words = p.page * W;
-  for (int64_t h = h0; h < h1; ++h) {
-    // Stage K rows (coalesced 16-byte loads) and copy V rows straight through.
-    for (int c = tid; c < kStoreTok * Q4; c += 256) {
-      const int t = c / Q4, q4 = c - t * Q4;
-      if (t < nt) {
-        const int64_t src = (i0 + t) * p.tok_stride_w + h * W + 4 * q4;
-        u32x4 kv = *reinterpret_cast<const u32x4*>(p.key + src);
-        kbuf[t * LD + 4 * q4 + 0] = kv.x;
-        kbuf[t * LD + 4 * q4 + 1] = kv.y;
-        kbuf[t * LD + 4 * q4 + 2] = kv.z;
-        kbuf[t * LD + 4 * q4 + 3] = kv.w;
-        const int64_t blk = s_blk[t];
-        if (blk >= 0) {
-          u32x4 vv = *reinterpret_cast<const u32x4*>(p.value + src);
-          const int64_t dst = ((blk * p.heads + h) * p.page + s_off[t]) * W + 4 * q4;
-          *reinterpret_cast<u32x4*>(p.vc + dst) = vv;
-        }
+  // Every K and V load of the block in flight at once (coalesced 16-byte loads:
+  // a token's rows of HB heads are contiguous); tokens that are not stored
+  // (padding slots, positions past the page table) are not read.
+  u32x4 kv[NCH], vv[NCH];
+  int64_t dst[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int idx = tid + 256 * c;
+    const int t = idx / (HB * Q4), rem = idx - t * (HB * Q4), hh = rem / Q4, q4 = rem - hh * Q4;
+    dst[c] = -1;
+    kv[c] = u32x4{0u, 0u, 0u, 0u};
+    vv[c] = u32x4{0u, 0u, 0u, 0u};
+    if (t < nt && h0 + hh < p.heads) {
+      int64_t blk, off;
+      store_target(p, i0 + t, blk, off);
+      if (blk >= 0) {
+        const int64_t src = (i0 + t) * p.tok_stride_w + (h0 + hh) * W + 4 * q4;
+        kv[c] = *reinterpret_cast<const u32x4*>(p.key + src);
+        vv[c] = *reinterpret_cast<const u32x4*>(p.value + src);
+        dst[c] = ((blk * p.heads + h0 + hh) * p.page + off) * W + 4 * q4;
       }
     }
-    __syncthreads();
-    // K: word w of token t -> w*P + off_t; 16 neighbouring lanes take the 16 tokens.
-    for (int idx = tid; idx < kStoreTok * W; idx += 256) {
-      const int t = idx & (kStoreTok - 1), w = idx / kStoreTok;
-      const int64_t blk = s_blk[t];
-      if (t < nt && blk >= 0)
-        p.kc[(blk * p.heads + h) * page_words + (int64_t)w * p.page + s_off[t]] = kbuf[t * LD + w];
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int idx = tid + 256 * c;
+    const int t = idx / (HB * Q4), rem = idx - t * (HB * Q4), hh = rem / Q4, q4 = rem - hh * Q4;
+    if (dst[c] >= 0) {
+      uint32_t* kr = &kbuf[hh][t * LD + 4 * q4];
+      kr[0] = kv[c].x;
+      kr[1] = kv[c].y;
+      kr[2] = kv[c].z;
+      kr[3] = kv[c].w;
+      *reinterpret_cast<u32x4*>(p.vc + dst[c]) = vv[c];
     }
-    __syncthreads();
+  }
+  __syncthreads();
+  const int64_t page_words = p.page * W;
+  // K: word w of token t -> w*P + off_t; 16 neighbouring lanes take the 16 tokens,
+  // so consecutive slots of one page become one 64-byte run per word row.
+  for (int idx = tid; idx < kStoreTok * W * HB; idx += 256) {
+    const int t = idx & (kStoreTok - 1), r = idx / kStoreTok, hh = r / W, w = r - hh * W;
+    const int64_t blk = s_blk[t];
+    if (t < nt && blk >= 0 && h0 + hh < p.heads)
+      p.kc[(blk * p.heads + h0 + hh) * page_words + (int64_t)w * p.page + s_off[t]] = kbuf[hh][t * LD + w];
   }
 }
 
 int store_launch(const StoreParams& sp, int W, hipStream_t stream) {
   if (sp.ntok == 0) return CA_OK;
-  const int64_t gx = cdiv(sp.ntok, kStoreTok);
-  if (gx > 0x7fffffff) return CA_DECLINED;
-  // Enough blocks to fill the chip: split the heads over grid.y when tokens are few.
-  int64_t gy = gx >= 2048 ? 1 : std::min<int64_t>(sp.heads, std::max<int64_t>(1, 2048 / gx));
-  StoreParams p = sp;
-  p.heads_per_block = (int)cdiv(sp.heads, gy);
-  gy = cdiv(sp.heads, p.heads_per_block);
-  dim3 grid((unsigned)gx, (unsigned)gy), block(256);
+  const int64_t nb = cdiv(sp.ntok, kStoreTok) * cdiv(sp.heads, 256 / W);
+  if (nb > 0x7fffffff) return CA_DECLINED;
+  dim3 grid((unsigned)nb), block(256);
   switch (W) {
-    case 16: hipLaunchKernelGGL(store_kernel<16>, grid, block, 0, stream, p); break;
-    case 32: hipLaunchKernelGGL(store_kernel<32>, grid, block, 0, stream, p); break;
-    case 64: hipLaunchKernelGGL(store_kernel<64>, grid, block, 0, stream, p); break;
-    case 128: hipLaunchKernelGGL(store_kernel<128>, grid, block, 0, stream, p); break;
+    case 16: hipLaunchKernelGGL(store_kernel<16>, grid, block, 0, stream, sp); break;
+    case 32: hipLaunchKernelGGL(store_kernel<32>, grid, block, 0, stream, sp); break;
+    case 64: hipLaunchKernelGGL(store_kernel<64>, grid, block, 0, stream, sp); break;
+    case 128: hipLaunchKernelGGL(store_kernel<128>, grid, block, 0, stream, sp); break;
     default: return CA_DECLINED;
   }
   return ca_launch_status();
