@@ -531,15 +531,18 @@ __global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
     //
     // Ping-pong: group 0 and group 1 share each SIMD and take turns, half a
     // tile apart, between an MFMA phase (the S MFMAs of tile t and the P.V
-    // MFMAs of tile t-1) and a VALU phase (the softmax of tile t); a block
-    // barrier ends every half-step h.  Group g runs its MFMA phase for tile t at
-    // h = 2t + g and its softmax of tile t at h = 2t + g + 1, so K(t) is read at
-    // h = 2t, 2t+1 and V(t) at h = 2t+2, 2t+3.  Each MFMA phase issues the next
-    // tile of its group's stream: group 0 K(t+2) at h = 2t (into the buffer of
-    // K(t-1), last read at h = 2t-1), group 1 V(t+1) at h = 2t+1 (into the
-    // buffer of V(t-2), last read at h = 2t-1).  The barrier that ends an odd h
-    // = 2t+1 first waits for all but each wave's latest tile: K(t+1) and V(t),
-    // read from h = 2t+2 on.
+    // MFMAs of tile t-1) and a VALU phase (the softmax of tile t).  Group g runs
+    // its MFMA phase for tile t at half-step h = 2t + g and its softmax of tile t
+    // at h = 2t + g + 1, so K(t) is read at h = 2t, 2t+1 and V(t) at h = 2t+2,
+    // 2t+3.  Each MFMA phase issues the next tile of its group's stream: group 0
+    // K(t+2) at h = 2t (into the buffer of K(t-1), last read at h = 2t-1),
+    // group 1 V(t+1) at h = 2t+1 (into the buffer of V(t-2), last read at
+    // h = 2t-1).  A block barrier ends every odd h = 2t+1, after each wave has
+    // waited for all but its latest tile (K(t+1) and V(t), read from h = 2t+2
+    // on).  Between two such barriers the waves read only tiles that landed
+    // before the first and write only buffers whose readers all ran before it,
+    // so no barrier is needed at even h; the groups keep their alternation by
+    // themselves (one barrier per tile was measured 3 % faster than two).
     if (nkt > 0) {
       constexpr int NL = C::NL;  // direct loads per wave and tile
       f32x16 st[2];
@@ -586,10 +589,7 @@ __global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
             bad |= !(ls <= kHeadSum);  // also NaN
           }
         }
-        if (h & 1)
-          loads_landed_barrier<NL>();
-        else
-          __syncthreads();
+        if (h & 1) loads_landed_barrier<NL>();
       }
       __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads past the range (zeros) have landed
     }
