@@ -238,7 +238,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs_kernel, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs_kernel / HBM_PEAK_GBS, 4),
                      "traffic": traffic_bytes("decode"),
-                     "kernel": "decode_tiles_kernel<128,bf16> + decode_tiles_combine_kernel<128,bf16> (one call)",
+                     "kernel": "decode_tiles_kernel<128,bf16> (one call: rows of up to 2048 keys merge in-block)",
                      "algorithmic_bytes": w["bytes"]},
     }
     del w

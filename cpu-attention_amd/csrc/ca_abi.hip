@@ -95,7 +95,7 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
     return CA_DECLINED;
   const int64_t need = ca_decode_workspace_bytes(a->num_seqs, a->num_heads, a->head_dim,
                                                  a->page_size, a->page_table_width);
-  if (!a->workspace || !aligned16(a->workspace) || a->workspace_bytes < need) return CA_DECLINED;
+  if (need > 0 && (!a->workspace || !aligned16(a->workspace) || a->workspace_bytes < need)) return CA_DECLINED;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t words = a->head_dim * esize(a->dtype) / 4;
 

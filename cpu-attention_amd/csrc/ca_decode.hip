@@ -8,13 +8,16 @@
 // past the last page in use.
 //
 // Work split.  One wave per 256-key tile of one row (sequence, head): grid.x walks
-// the rows, grid.y the tile groups (4 tiles per 256-thread block) up to the page
-// table's capacity, so every row's first tiles are dispatched first and tiles
-// past a row's length exit at once.  A row that fits one tile is written by that
-// tile; otherwise each tile leaves a partial (max, sum, P.V) and the combine
-// kernel merges them.  The host needs no lengths and nothing synchronises.  (A
-// stream-K split into equal slices per resident wave was measured slower: 347 us
-// against 189 us on the bench's batch.)
+// the rows, grid.y the tile groups (8 tiles, 2048 keys, per 512-thread block) up
+// to the page table's capacity, so every row's first tiles are dispatched first;
+// waves whose tile is past the row's length exit at once (a block barrier waits
+// only for the waves still running).  The waves of a block merge their partial
+// (max, sum, P.V) states in LDS: a row of up to 2048 keys is written by its one
+// block, with no workspace traffic and no second kernel.  Longer rows leave one
+// partial per block in the workspace, and the combine kernel merges those.  The
+// host needs no lengths and nothing synchronises.  (A stream-K split into equal
+// slices per resident wave was measured slower: 347 us against 189 us on the
+// bench's batch.)
 //
 // Layout use (the reference's PageLayout, :58-130): a 16-key unit never straddles a
 // page (P % 16 == 0), so a tile is up to 16 units, each one contiguous run inside one
@@ -34,6 +37,7 @@ namespace ca {
 
 constexpr int kTile = 256;    // keys per tile
 constexpr int kUnit = 16;     // keys per unit (one page run)
+constexpr int kDecWaves = 8;  // tiles (waves) per block
 
 // out[idx .. idx+N) = v * inv in the output dtype (bf16: round to nearest even).
 template <int N, bool BF>
@@ -246,11 +250,10 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
   }
 }
 
-// Ends a piece of a row: reduce the lane partials and write either the output
-// (the piece was the whole row) or a partial into workspace slot `slot`.
+// Reduces a wave's lane partials into part[E + 2] in LDS: acc over the lane
+// groups (lanes with the same dims), l over the wave, and the wave's max.
 template <int E, bool BF>
-__device__ __forceinline__ void finish_piece(const DecodeParams& p, RowState<E, BF>& st,
-                                             int64_t row, bool whole, int64_t slot) {
+__device__ __forceinline__ void wave_partial(RowState<E, BF>& st, float* part) {
   using D = DecodeShape<E, BF>;
   constexpr int DPL = D::DPL, LPR = D::LPR;
   const int lane = threadIdx.x & 63;
@@ -260,89 +263,117 @@ __device__ __forceinline__ void finish_piece(const DecodeParams& p, RowState<E, 
 #pragma unroll
     for (int i = 0; i < DPL; ++i) st.acc[i] += __shfl_xor(st.acc[i], o);
   if (lane < LPR) {
-    if (whole) {
-      store_out<DPL, BF>(p.out, row * E + lane * DPL, st.acc, l > 0.f ? 1.f / l : 0.f);
-    } else {
-      float* pa = p.part_acc + slot * E + lane * DPL;
 #pragma unroll
-      for (int i = 0; i < DPL; i += 4)
-        *reinterpret_cast<f32x4*>(pa + i) = f32x4{st.acc[i], st.acc[i + 1], st.acc[i + 2], st.acc[i + 3]};
-      if (lane == 0) {
-        p.part_ml[2 * slot] = st.m;
-        p.part_ml[2 * slot + 1] = l;
-      }
+    for (int i = 0; i < DPL; ++i) part[lane * DPL + i] = st.acc[i];
+    if (lane == 0) {
+      part[E] = st.m;
+      part[E + 1] = l;
     }
   }
 }
 
-// One wave per 256-key tile of each row.
-template <int E, bool BF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
-void decode_tiles_kernel(DecodeParams p) {
-  __shared__ __attribute__((aligned(16))) float p_lds[4][kTile];
-  const int wv = threadIdx.x >> 6;
-  const int64_t row = blockIdx.x;
-  const int64_t s = row / p.heads, h = row - s * p.heads;
-  const int64_t tile = (int64_t)blockIdx.y * 4 + wv;
-  const int64_t len = row_len(p, s);
-  const int64_t t0 = tile * kTile;
-  if (t0 >= len) return;
-  RowState<E, BF> st;
-  st.init();
-  decode_tile<E, BF>(p, s, h, t0, (int)min<int64_t>(kTile, len - t0), p_lds[wv], st);
-  finish_piece<E, BF>(p, st, row, len <= kTile, row * p.tiles + tile);
+// Merges n partial states (m_t, l_t, acc_t) with weights 2^(m_t - M): lane-wise
+// dims lane*DPC.., returns the merged sum; acc gets the merged P.V.
+template <int E, int DPC, typename Get>
+__device__ __forceinline__ float merge_states(int n, Get&& get, float& mx, float (&acc)[DPC]) {
+  const int lane = threadIdx.x & 63;
+  mx = -INFINITY;
+  for (int t = 0; t < n; ++t) mx = fmaxf(mx, get(t, -1));
+#pragma unroll
+  for (int i = 0; i < DPC; ++i) acc[i] = 0.f;
+  float l = 0.f;
+  if (mx == -INFINITY) return 0.f;  // nothing readable
+  for (int t = 0; t < n; ++t) {
+    const float wgt = __builtin_amdgcn_exp2f(get(t, -1) - mx);
+    l = fmaf(wgt, get(t, -2), l);
+    if (lane * DPC < E) {
+#pragma unroll
+      for (int i = 0; i < DPC; ++i) acc[i] = fmaf(wgt, get(t, lane * DPC + i), acc[i]);
+    }
+  }
+  return l;
 }
 
+// One wave per 256-key tile of each row, 8 tiles per block merged in LDS.
+template <int E, bool BF>
+__global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(4)))
+void decode_tiles_kernel(DecodeParams p) {
+  __shared__ __attribute__((aligned(16))) float p_lds[kDecWaves][kTile];
+  __shared__ float part[kDecWaves][E + 2];
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = blockIdx.x;
+  const int64_t s = row / p.heads, h = row - s * p.heads;
+  const int64_t tile = (int64_t)blockIdx.y * kDecWaves + wv;
+  const int64_t len = row_len(p, s);
+  const int64_t t0 = tile * kTile;
+  // Waves past the row's end exit (whole waves: the barrier below waits for the
+  // others only), except the first wave of the row, which writes a row with no
+  // key as exactly 0.
+  if (t0 >= len && tile != 0) return;
+  RowState<E, BF> st;
+  st.init();
+  if (t0 < len) decode_tile<E, BF>(p, s, h, t0, (int)min<int64_t>(kTile, len - t0), p_lds[wv], st);
+  wave_partial<E, BF>(st, part[wv]);
+  __syncthreads();
+  if (wv != 0) return;
+  constexpr int DPC = E >= 64 ? E / 64 : 1;
+  const int lane = threadIdx.x & 63;
+  const int n = (int)max<int64_t>(1, min<int64_t>(kDecWaves, cdiv(len, kTile) - (int64_t)blockIdx.y * kDecWaves));
+  float mx, acc[DPC];
+  const float l = merge_states<E, DPC>(n, [&](int t, int i) {
+    return part[t][i == -1 ? E : (i == -2 ? E + 1 : i)];
+  }, mx, acc);
+  if (blockIdx.y == 0 && len <= kDecWaves * kTile) {
+    if (lane * DPC < E) store_out<DPC, BF>(p.out, row * E + lane * DPC, acc, l > 0.f ? 1.f / l : 0.f);
+  } else {
+    const int64_t slot = row * cdiv(p.tiles, kDecWaves) + blockIdx.y;
+    if (lane * DPC < E) {
+#pragma unroll
+      for (int i = 0; i < DPC; ++i) p.part_acc[slot * E + lane * DPC + i] = acc[i];
+    }
+    if (lane == 0) {
+      p.part_ml[2 * slot] = mx;
+      p.part_ml[2 * slot + 1] = l;
+    }
+  }
+}
+
+// One wave per row longer than one block: merges the blocks' partials.
 template <int E, bool BF>
 __global__ __launch_bounds__(256) void decode_tiles_combine_kernel(DecodeParams p) {
   constexpr int DPC = E >= 64 ? E / 64 : 1;
-  constexpr int ACTIVE = E / DPC;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= p.nseqs * p.heads) return;
   const int64_t len = row_len(p, row / p.heads);
-  if (len > 0 && len <= kTile) return;  // written by the tile itself
-  float acc[DPC];
-#pragma unroll
-  for (int i = 0; i < DPC; ++i) acc[i] = 0.f;
-  float inv = 0.f;
-  if (len > 0) {
-    const int64_t nt = cdiv(len, kTile);
-    const float* ml = p.part_ml + row * p.tiles * 2;
-    float mx = -INFINITY;
-    for (int64_t t = lane; t < nt; t += kWave) mx = fmaxf(mx, ml[2 * t]);
-    mx = wave_max(mx);
-    if (mx != -INFINITY) {
-      float l = 0.f;
-      const float* pa = p.part_acc + row * p.tiles * E + lane * DPC;
-      for (int64_t t = 0; t < nt; ++t) {
-        const float wgt = __builtin_amdgcn_exp2f(ml[2 * t] - mx);
-        l = fmaf(wgt, ml[2 * t + 1], l);
-        if (lane < ACTIVE) {
-#pragma unroll
-          for (int i = 0; i < DPC; ++i) acc[i] = fmaf(wgt, pa[t * E + i], acc[i]);
-        }
-      }
-      inv = l > 0.f ? 1.f / l : 0.f;
-    }
-  }
-  if (lane < ACTIVE) store_out<DPC, BF>(p.out, row * E + lane * DPC, acc, inv);
+  if (len <= kDecWaves * kTile) return;  // written by its block
+  const int64_t nb = cdiv(p.tiles, kDecWaves);
+  const float* ml = p.part_ml + row * nb * 2;
+  const float* pa = p.part_acc + row * nb * E;
+  float mx, acc[DPC];
+  const float l = merge_states<E, DPC>((int)cdiv(len, kDecWaves * kTile), [&](int t, int i) {
+    return i == -1 ? ml[2 * t] : (i == -2 ? ml[2 * t + 1] : pa[t * E + i]);
+  }, mx, acc);
+  if (lane * DPC < E) store_out<DPC, BF>(p.out, row * E + lane * DPC, acc, l > 0.f ? 1.f / l : 0.f);
 }
 
 int64_t decode_tiles(int64_t pt_width, int64_t page) { return cdiv(pt_width * page, kTile); }
 
-// Partial slots the workspace must hold: one per (row, tile).
-int64_t decode_workspace_slots(int64_t rows, int64_t tiles) { return rows * tiles; }
+// Partial slots the workspace must hold: one per (row, block of 8 tiles) when
+// rows can outgrow one block, none otherwise.
+int64_t decode_workspace_slots(int64_t rows, int64_t tiles) {
+  return tiles > kDecWaves ? rows * cdiv(tiles, kDecWaves) : 0;
+}
 
 template <int E, bool BF>
 static int decode_launch_t(const DecodeParams& p, hipStream_t stream) {
   const int64_t rows = p.nseqs * p.heads;
-  const int64_t gy = cdiv(p.tiles, 4);
-  if (rows > 0x7fffffff || gy > 65535 || rows * p.tiles > p.slots) return CA_DECLINED;
-  hipLaunchKernelGGL((decode_tiles_kernel<E, BF>), dim3((unsigned)rows, (unsigned)gy), dim3(256), 0,
+  const int64_t gy = cdiv(p.tiles, kDecWaves);
+  if (rows > 0x7fffffff || gy > 65535 || decode_workspace_slots(rows, p.tiles) > p.slots) return CA_DECLINED;
+  hipLaunchKernelGGL((decode_tiles_kernel<E, BF>), dim3((unsigned)rows, (unsigned)gy), dim3(64 * kDecWaves), 0,
                      stream, p);
   int st = ca_launch_status();
-  if (st != CA_OK) return st;
+  if (st != CA_OK || gy == 1) return st;
   hipLaunchKernelGGL((decode_tiles_combine_kernel<E, BF>), dim3((unsigned)cdiv(rows, 4)), dim3(256),
                      0, stream, p);
   return ca_launch_status();

@@ -93,8 +93,11 @@ def test_entries_decline_malformed_calls_without_a_gpu():
     assert lib.ca_flash(ctypes.byref(f), None) == K.CA_DECLINED  # seq_q < 1
     f.seq_q = 4
     assert lib.ca_flash(ctypes.byref(f), None) == K.CA_DECLINED  # null pointers
-    assert lib.ca_decode_workspace_bytes(64, 32, 128, 32, 64) == \
-        ((64 * 32 * 8 * 128 * 4 + 255) // 256) * 256 + 64 * 32 * 8 * 2 * 4
+    # decode: one (max, sum, P.V) partial per (row, block of 8 tiles of 256 keys), and
+    # none when a row fits one block (2048 keys)
+    assert lib.ca_decode_workspace_bytes(64, 32, 128, 32, 64) == 0
+    assert lib.ca_decode_workspace_bytes(64, 32, 128, 32, 65) == \
+        ((64 * 32 * 2 * 128 * 4 + 255) // 256) * 256 + 64 * 32 * 2 * 2 * 4
     assert lib.ca_flash_workspace_bytes(1, 1, 1, 1, 64, 1) == 0
 
 
