@@ -51,9 +51,9 @@ COPY_BYTES = 1 << 30  # the calibration copy of --profile-pass
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of --profile-pass on
 # MI355X: the calibration copy, then the decode kernels and the prefill kernel.
 TRAFFIC = {
-    "copy": {"fetch_kib": 524308.6, "write_kib": 1048576.0},
-    "decode": {"fetch_kib": 543470.8 + 2379.0, "write_kib": 4796.9 + 424.0},  # tiles + combine
-    "prefill": {"fetch_kib": 321530.4, "write_kib": 174200.5},
+    "copy": {"fetch_kib": 524307.7, "write_kib": 1048576.0},
+    "decode": {"fetch_kib": 543466.4, "write_kib": 512.0},
+    "prefill": {"fetch_kib": 311213.3, "write_kib": 174331.6},
 }
 
 
