@@ -264,10 +264,20 @@ struct Bf16Rows {
   int li, hf, lane, r0;
 
   __device__ __forceinline__ void load_q(const Bf16Pass& a) {
-    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(a.q + (int64_t)r0 * a.qs1, ((int64_t)(a.L - 1 - r0) * a.qs1 + E) * 2);
+    issue_q(a, r0);
+    reset();
+  }
+
+  // The Q loads of the 32 rows from `row0` alone (the accumulators may still
+  // hold the previous pass, whose rows r0 names).
+  __device__ __forceinline__ void issue_q(const Bf16Pass& a, int row0) {
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(a.q + (int64_t)row0 * a.qs1, ((int64_t)(a.L - 1 - row0) * a.qs1 + E) * 2);
 #pragma unroll
     for (int s = 0; s < NS; ++s)
       qr[s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (li * a.qs1 + 16 * s + 8 * hf) * 2, 0, 0));
+  }
+
+  __device__ __forceinline__ void reset() {
 #pragma unroll
     for (int d = 0; d < ND; ++d) o[d] = f32x16{};
     m = -INFINITY;
@@ -356,10 +366,19 @@ struct Bf16Rows {
   template <bool PV, bool S, typename F>
   __device__ __forceinline__ void mfma_phase(const uint16_t* vb, const bf16x8 (&pb)[4], const uint16_t* kb,
                                              f32x16 (&st)[2], F&& mid) {
-    constexpr int NPV = PV ? 4 * ND : 0, NOP = NPV + (S ? 2 * NS : 0), LA = 8, R = LA + 1;
+    constexpr int NPV = PV ? 4 * ND : 0, NS2 = S ? 2 * NS : 0, NOP = NPV + NS2, LA = 8, R = LA + 1;
     mid();
     __builtin_amdgcn_sched_barrier(0);
     bf16x8 buf[R];
+    // Stream position i -> operation: P.V MFMAs (< NPV) and S MFMAs alternate
+    // while both remain, so the two transposed V reads of a P.V MFMA and the one
+    // K read of an S MFMA spread evenly over the phase (the V reads alone, back to
+    // back, would keep the LDS busy for as long as their MFMAs take).
+    auto op = [](int i) {
+      constexpr int both = 2 * (NPV < NS2 ? NPV : NS2);
+      if (i < both) return (i & 1) ? NPV + (i >> 1) : (i >> 1);
+      return (NPV > NS2 ? 0 : NPV) + both / 2 + (i - both);  // the rest of the longer kind
+    };
     auto read = [&](int i) {
       if (i < NPV) return v_operand<E>(vb, lane, i / ND, i % ND);
       const int j = i - NPV;
@@ -367,16 +386,54 @@ struct Bf16Rows {
     };
 #pragma unroll
     for (int i = 0; i < NOP + LA; ++i) {
-      if (i < NOP) buf[i % R] = read(i);
-      const int k = i - LA;
-      if (k >= 0) {
+      if (i < NOP) buf[i % R] = read(op(i));
+      const int k0 = i - LA;
+      if (k0 >= 0) {
+        const int k = op(k0);
         if (k < NPV) {
-          o[k % ND] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(buf[k % R], pb[k / ND], o[k % ND], 0, 0, 0);
+          o[k % ND] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(buf[k0 % R], pb[k / ND], o[k % ND], 0, 0, 0);
         } else {
           const int j = k - NPV, kt = j & 1, s = j >> 1;
-          st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(buf[k % R], qr[s], s == 0 ? f32x16{} : st[kt], 0, 0, 0);
+          st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(buf[k0 % R], qr[s], s == 0 ? f32x16{} : st[kt], 0, 0, 0);
         }
-        if ((k & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        if ((k0 & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
+  // Bytes of LDS that store_staged needs per wave: 16 rows of E bf16, padded.
+  static constexpr int kStageRow = 2 * E + 16;
+  static constexpr int kStageBytes = 16 * kStageRow;
+
+  // out = acc / l, staged through this wave's `stage` area of LDS.  In the O^T
+  // layout a lane holds 4-dim runs of one row, so direct stores would touch 32
+  // rows per instruction with 16 bytes each; staged, each store instruction
+  // writes whole rows (64 / (E/8) rows of E/8 16-byte chunks).  Two rounds of 16
+  // rows; the area is private to the wave, whose LDS accesses run in order.
+  // A row with no visible key is 0.
+  __device__ __forceinline__ void store_staged(const Bf16Pass& a, char* stage) const {
+    constexpr int CPR = E / 8, RPI = 64 / CPR;  // 16-byte chunks per row, rows per store
+    const float lt = l + __shfl_xor(l, 32);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    const int ch = lane % CPR, rr0 = lane / CPR;
+#pragma unroll
+    for (int rnd = 0; rnd < 2; ++rnd) {
+      if ((li >> 4) == rnd) {
+        char* rowp = stage + (li & 15) * kStageRow;
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            u32x2 w = {pack_bf16x2(o[d][4 * q] * inv, o[d][4 * q + 1] * inv),
+                       pack_bf16x2(o[d][4 * q + 2] * inv, o[d][4 * q + 3] * inv)};
+            *reinterpret_cast<u32x2*>(rowp + (32 * d + 8 * q + 4 * hf) * 2) = w;
+          }
+      }
+#pragma unroll
+      for (int k = 0; k < 16 / RPI; ++k) {
+        const int rr = rr0 + RPI * k, row = r0 + 16 * rnd + rr;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stage + rr * kStageRow + ch * 16);
+        if (row < a.L) *reinterpret_cast<u32x4*>(a.out + (int64_t)row * a.heads * E + ch * 8) = v;
       }
     }
   }
@@ -509,18 +566,46 @@ __global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
   w.li = lane & 31;
   w.hf = lane >> 5;
 
-  for (int pass = 0; pass < pw.n; ++pass) {
-    const int q0 = (int)(pass == 0 ? pw.qb0 : pw.qb1) * BM;
-    w.r0 = q0 + 32 * wv;  // first row of this wave
-    const int kend_b = p.causal ? min(S, q0 + BM + diag) : S;
-    const int nkt = kend_b > 0 ? (kend_b + BN - 1) / BN : 0;
-    const int kend_w = p.causal ? min(S, w.r0 + 32 + diag) : S;
-    const int nkt_w = kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
-    a.q0 = q0;
-    a.kend = kend_b;
+  // A pass: query block qb (rows q0..q0+BM-1), key tiles up to kend_b for the
+  // block and kend_w for this wave.
+  struct Geo {
+    int q0, kend_b, nkt, nkt_w;
+  };
+  auto geo = [&](int pass) {
+    Geo g;
+    g.q0 = (int)(pass == 0 ? pw.qb0 : pw.qb1) * BM;
+    g.kend_b = p.causal ? min(S, g.q0 + BM + diag) : S;
+    g.nkt = g.kend_b > 0 ? (g.kend_b + BN - 1) / BN : 0;
+    const int kend_w = p.causal ? min(S, g.q0 + 32 * wv + 32 + diag) : S;
+    g.nkt_w = kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
+    return g;
+  };
+  TileStream<E> ts;
+  // The first tiles of a pass: K(j) goes to buffer j % 3; V(-1) (zeros: the
+  // P.V at t = 0 has p = 0, and 0 * a stale NaN would not be 0) to buffer 2,
+  // V(j) to buffer j % 3.  K buffer 2 and V buffer 1 stay free until the walk.
+  auto prologue = [&](const Geo& g) {
+    ts.init(wg ? a.v : a.k, wg ? a.vs1 : a.ks1, g.kend_b, wg ? Vs : Ks, C::NBUF, wg ? 2 : 0, wv4);
+    if (wg)
+      ts.issue_zeros(off);
+    else
+      ts.issue(off);
+    ts.issue(off);
+  };
+  // This wave's output staging area: in K buffer 2 (group 0) or V buffer 1
+  // (group 1), which the next pass's prologue leaves alone.
+  static_assert(C::NWG * Bf16Rows<E>::kStageBytes <= C::TBUF * 2, "staging fits a tile buffer");
+  char* stage = reinterpret_cast<char*>(wg ? Vs + C::TBUF : Ks + 2 * C::TBUF) + wv4 * Bf16Rows<E>::kStageBytes;
 
-    if (pass > 0) __syncthreads();  // every wave is done with the previous pass's tiles
-    w.load_q(a);
+  Geo g = geo(0);
+  a.q0 = g.q0;
+  a.kend = g.kend_b;
+  w.r0 = g.q0 + 32 * wv;
+  w.load_q(a);
+  if (g.nkt > 0) prologue(g);
+  uint32_t bad_passes = 0;  // bit p: this wave's rows of pass p need the safe pass
+  for (int pass = 0; pass < pw.n; ++pass) {
+    const int nkt = g.nkt, nkt_w = g.nkt_w;
     bool bad = false;
 
     // The fast walk.  The row max is fixed at tile 0's (every row that sees any
@@ -551,15 +636,6 @@ __global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
       for (int cc = 0; cc < 4; ++cc) pb[cc] = bf16x8{};
       auto kbuf = [&](int t) { return Ks + (t % C::NBUF) * C::TBUF; };
       auto vbuf = [&](int t) { return Vs + ((t + C::NBUF) % C::NBUF) * C::TBUF; };
-      TileStream<E> ts;
-      // K(j) goes to buffer j % 3; V(-1) (zeros: the P.V at t = 0 has p = 0,
-      // and 0 * a stale NaN would not be 0) to buffer 2, V(j) to buffer j % 3.
-      ts.init(wg ? a.v : a.k, wg ? a.vs1 : a.ks1, kend_b, wg ? Vs : Ks, C::NBUF, wg ? 2 : 0, wv4);
-      if (wg)
-        ts.issue_zeros(off);
-      else
-        ts.issue(off);
-      ts.issue(off);
       loads_done_barrier();
       auto next_tile = [&] { ts.issue(off); };
       for (int h = 0; h < 2 * nkt + 2; ++h) {
@@ -593,11 +669,45 @@ __global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
       }
       __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads past the range (zeros) have landed
     }
+    __syncthreads();  // every wave's tile loads have landed: all buffers are free
     bad = __any(bad);
+    // The next pass's Q and first tiles go out now, so that their latency
+    // overlaps this pass's output stores.
+    const bool more = pass + 1 < pw.n;
+    Geo gn = g;
+    if (more) {
+      gn = geo(pass + 1);
+      w.issue_q(a, gn.q0 + 32 * wv);
+      if (gn.nkt > 0) prologue(gn);
+    }
     // A wave whose fast walk recorded an overflow risk leaves its rows to the
-    // safe pass.
-    if (!bad) w.store(a);
-    if (__syncthreads_or(bad)) bf16_safe_pass<E>(a, bad);
+    // safe pass, after the last pass.
+    if (bad)
+      bad_passes |= 1u << pass;
+    else
+      w.store_staged(a, stage);
+    if (more) {
+      g = gn;
+      a.q0 = g.q0;
+      a.kend = g.kend_b;
+      w.r0 = g.q0 + 32 * wv;
+      w.reset();
+    }
+  }
+  // Rare: rows whose logits outgrew the fast walk's fixed max, redone with a
+  // running max once every pass is through (no register of the walk lives
+  // across the out-of-line call).  Every wave takes part in the barriers.
+  if (__syncthreads_or(bad_passes != 0)) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+    for (int pass = 0; pass < pw.n; ++pass) {
+      const Geo gp = geo(pass);
+      a.q0 = gp.q0;
+      a.kend = gp.kend_b;
+      const bool act = (bad_passes >> pass) & 1;
+      if (__syncthreads_or(act)) bf16_safe_pass<E>(a, act);
+      __syncthreads();
+    }
   }
 }
 
