@@ -53,7 +53,7 @@ COPY_BYTES = 1 << 30  # the calibration copy of --profile-pass
 TRAFFIC = {
     "copy": {"fetch_kib": 524307.7, "write_kib": 1048576.0},
     "decode": {"fetch_kib": 543466.4, "write_kib": 512.0},
-    "prefill": {"fetch_kib": 311213.3, "write_kib": 174331.6},
+    "prefill": {"fetch_kib": 325223.0, "write_kib": 174080.0},
 }
 
 
