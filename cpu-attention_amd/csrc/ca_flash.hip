@@ -361,8 +361,9 @@ struct Bf16Rows {
   // as one stream of MFMAs whose LDS operand reads run LA operands ahead, in
   // scheduling regions of 4 MFMAs.  The lookahead keeps the LDS latency off the
   // MFMA pipe; the regions keep the compiler from hoisting every read (which
-  // would not fit in a wave's 256 registers).  `mid` runs after the first
-  // region (the wave's tile loads, issued while its first MFMAs execute).
+  // would not fit in a wave's 256 registers).  `mid` (the wave's tile loads)
+  // runs first, in a region of its own: placed inside the stream it cost
+  // registers across the loop.
   template <bool PV, bool S, typename F>
   __device__ __forceinline__ void mfma_phase(const uint16_t* vb, const bf16x8 (&pb)[4], const uint16_t* kb,
                                              f32x16 (&st)[2], F&& mid) {
