@@ -1,4 +1,4 @@
-"""The serving steps inside a HIP graph: decode, store and prompt append, as the
+"""The serving steps inside a HIP graph: decode, store, prompt append and prefill, as the
 reference's engine use (examples/ops.py:19-31) would replay a captured step.  With
 host checks off a valid call reads nothing on the host, synchronises nothing and
 allocates only through torch (from the graph's pool while capturing), so it
@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from cpu_attention import _kernel as K
-from cpu_attention import flash_attn_with_kvcache, reshape_and_cache
+from cpu_attention import flash_attn_func, flash_attn_with_kvcache, reshape_and_cache
 from helpers import stage
 
 pytestmark = pytest.mark.gpu
@@ -149,3 +149,23 @@ def test_prompt_append_replays(cuda, dtype, no_host_checks):
         assert torch.isfinite(out).all()
         assert same_bytes(out, ref)
         assert same_bytes(kc, kr) and same_bytes(vc, vr)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("sq,sk", [(300, 300), (3, 3000)])
+def test_flash_attn_func_replays(cuda, dtype, sq, sk):
+    """Prefill: the tiled route and the few-rows route, whose split-K workspace the
+    warm-up calls before the capture have already grown."""
+    b, h, d = 2, 4, 64
+    q, k, v = (torch.zeros(b, n, h, d, dtype=dtype, device=cuda) for n in (sq, sk, sk))
+    graph, out = capture(lambda: flash_attn_func(q, k, v, causal=True))
+    g = torch.Generator(device=cuda).manual_seed(9)
+    for _ in range(3):
+        for t in (q, k, v):
+            t.copy_(torch.randn(t.shape, generator=g, device=cuda).to(dtype))
+        ref = flash_attn_func(q.clone(), k.clone(), v.clone(), causal=True)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all()
+        assert same_bytes(out, ref)
