@@ -146,3 +146,26 @@ def test_logits_outgrowing_the_first_tile(cuda, d, causal):
     out = flash_attn_func(q, k, v, causal=causal)
     ref = attention(values(q), values(k), values(v), d ** -0.5, causal)
     assert_close(out, ref, torch.bfloat16, paged=False)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("bad_pass", [0, 1])
+def test_safe_pass_for_one_pass_of_a_causal_pair(cuda, d, bad_pass):
+    """A causal call of two 256-row query blocks runs as one pair in one bf16 block:
+    pass 0 (rows 256-511), then pass 1 (rows 0-255).  Only one of the two passes
+    holds rows whose logits outgrow the fast walk's fixed max; the block redoes
+    exactly those after both passes and keeps the other pass's fast results."""
+    g = torch.Generator().manual_seed(12 + bad_pass)
+    b, L, h = 1, 512, 2
+    q = torch.randn(b, L, h, d, generator=g) * 0.5 + 1.0
+    k = torch.randn(b, L, h, d, generator=g) * 0.5
+    if bad_pass == 0:
+        k[:, 400] = 6.0  # seen only by rows >= 400 (pass 0)
+    else:
+        k[:, 200] = 6.0  # seen by every row >= 200: rows of pass 0 get q < 0 for it
+        q[:, 256:] = -q[:, 256:]
+    q, k = q.bfloat16().to(cuda), k.bfloat16().to(cuda)
+    v = torch.randn(b, L, h, d, generator=g).bfloat16().to(cuda)
+    out = flash_attn_func(q, k, v, causal=True)
+    ref = attention(values(q), values(k), values(v), d ** -0.5, True)
+    assert_close(out, ref, torch.bfloat16, paged=False)
