@@ -157,7 +157,14 @@ def _on_gpu(device, *ts):
     return all(t.is_cuda and t.device == device for t in ts)
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device):
+    """torch's current stream on ``device`` as a raw handle (the direct query when
+    this torch has it: it skips building a Stream object on every call)."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -186,6 +193,9 @@ class Module:
 
     def __init__(self, lib):
         self.lib = lib
+        # Workspace sizes are pure functions of the shapes: asked once per shape.
+        self._dec_ws = {}
+        self._flash_ws = {}
 
     def _raise(self, rc, what):
         msg = self.lib.ca_status_string(rc).decode()
@@ -286,8 +296,11 @@ class Module:
         if slots is not None:
             slots = _index_on(slots, dev)
         out = dst if dst is not None else torch.empty(q.shape, dtype=q.dtype, device=dev)
-        ws_bytes = self.lib.ca_decode_workspace_bytes(b, heads, hd, page, width)
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        key = (b, heads, hd, page, width)
+        ws_bytes = self._dec_ws.get(key)
+        if ws_bytes is None:
+            ws_bytes = self._dec_ws[key] = self.lib.ca_decode_workspace_bytes(*key)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
         args = DecodeArgs(
             q=q.data_ptr(), q_stride=q_stride, k_cache=k_cache.data_ptr(),
             v_cache=v_cache.data_ptr(), k_new=k.data_ptr() if store else None,
@@ -296,7 +309,8 @@ class Module:
             page_table=page_table.data_ptr(), page_table_width=width, out=out.data_ptr(),
             num_seqs=b, num_heads=heads, head_dim=hd, page_size=page, num_blocks=nblocks,
             scale=float(hd) ** -0.5 if scale is None else float(scale), dtype=DTYPES[q.dtype],
-            workspace=ws.data_ptr(), workspace_bytes=ws.numel(), new_tokens=n if store else 0)
+            workspace=ws.data_ptr() if ws is not None else None, workspace_bytes=ws_bytes,
+            new_tokens=n if store else 0)
         rc = self.lib.ca_decode(ctypes.byref(args), _stream(dev))
         if rc == CA_DECLINED:
             return None
@@ -350,6 +364,13 @@ class Module:
 
     # -- flash ----------------------------------------------------------------
     def flash_workspace_bytes(self, q, k):
+        key = (q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3], q.dtype)
+        need = self._flash_ws.get(key)
+        if need is None:
+            need = self._flash_ws[key] = self._flash_ws_query(q, k)
+        return need
+
+    def _flash_ws_query(self, q, k):
         return self.lib.ca_flash_workspace_bytes(q.shape[0], q.shape[1], k.shape[1], q.shape[2],
                                                  q.shape[3], DTYPES.get(q.dtype, 0))
 
