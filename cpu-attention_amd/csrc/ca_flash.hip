@@ -29,6 +29,10 @@ namespace ca {
 
 constexpr int kBM = 128;  // fp32: query rows per block (4 waves x 32)
 
+#ifndef CA_FLASH_P64
+#define CA_FLASH_P64 1
+#endif
+
 // A raw buffer resource over [base, base + bytes): loads past `bytes` return 0.
 // The per-tile K/V loads rebase the resource at each tile, so their per-lane
 // offsets stay fixed across the loop (no address registers rewritten under
@@ -104,6 +108,7 @@ struct FlashBf16Cfg {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4v;
 typedef __attribute__((address_space(3))) bf16x4v lds_bf16x4;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 
 // One bf16 block's work: a (batch, head) and one or two query blocks.  Causal
 // calls pair query block j with nqb-1-j, so every block walks about the same
@@ -713,6 +718,495 @@ __global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// bf16, 64 query rows per wave, softmax overlapped with the MFMAs
+// ---------------------------------------------------------------------------
+// Block = 4 waves x 64 query rows (the same 256-row query blocks as
+// flash_bf16_kernel), one wave per SIMD with the whole register file: Q and the
+// O accumulators live in AGPRs (only MFMAs read them), S, P and the operands in
+// VGPRs.  A wave's VALU work runs while its own MFMAs execute (measured on
+// gfx950: 4 MFMAs and 64 independent VALU ops per iteration take as long as the
+// VALU ops alone), so iteration t of the tile walk issues one interleaved stream
+//   the P.V MFMAs of tile t-1 and the S MFMAs of tile t+1 (64 at E = 128), and
+//   the softmax of tile t (one score per MFMA at E = 128),
+// with the S of consecutive tiles in two register sets.  Each K operand read
+// from LDS feeds the S MFMAs of both 32-row column blocks, and each V^T operand
+// both P.V MFMAs: half the LDS operand bytes per MFMA of the 32-row layout.
+// The MFMAs are inline assembly (for the AGPR operands), so the compiler does
+// not know their result latency: where a VALU read of an MFMA result follows
+// closely, mfma_guard() supplies the wait states.
+template <int E>
+struct FlashP64Cfg {
+  static constexpr int NW = 4;        // waves per block
+  static constexpr int BM = 64 * NW;  // query rows per block
+  static constexpr int BN = FlashBf16Cfg<E>::BN;
+  static constexpr int NL = FlashBf16Cfg<E>::NL;  // direct loads per wave and tile (K or V)
+  static constexpr int TBUF = FlashBf16Cfg<E>::TBUF;
+  static constexpr int NBUF = 3;
+  static constexpr int LDS_BYTES = NBUF * 2 * TBUF * 2;
+  static_assert(NW == FlashBf16Cfg<E>::NWG, "the tile loads are split over NWG waves");
+};
+
+// 64 query rows of one (batch, head) as two 32-row column blocks cb: lane (query
+// li, half hf) of block cb holds row r0 + 32 cb + li.
+template <int E>
+struct P64Rows {
+  static constexpr int BN = FlashP64Cfg<E>::BN, NS = E / 16, ND = E / 32;
+  static constexpr int NPV = 4 * ND;  // V^T operands of a tile: keys 16cc.., dims 32d..
+  static constexpr int NSK = 2 * NS;  // K operands of a tile: keys 32kt.., dims 16s..
+  static constexpr int LA = 6;        // operand reads run LA operands ahead of their MFMAs
+  static constexpr int NPRE = LA < NPV ? LA : NPV;  // V^T operands read ahead across a barrier
+  bf16x8 qr[2][NS];    // Q^T of column block cb as B operands (AGPRs)
+  f32x16 o[2][ND];     // O^T accumulators (AGPRs): dims 32d + 8(r/4) + 4hf + r%4
+  f32x16 st[2][2][2];  // S^T of two consecutive tiles: [tile parity][cb][kt]
+  bf16x8 pb[2][4];     // P^T of the latest softmax: [cb][16-key group cc]
+  bf16x8 opn[NPRE];    // the next iteration's first V^T operands, read before the barrier
+  float m[2], nmu[2], l[2];
+  int li, hf, lane, r0;
+  int klo, vlo;  // this lane's byte offsets of its K and V^T operand reads in a tile buffer
+
+  __device__ __forceinline__ void init(int lane_) {
+    lane = lane_;
+    li = lane & 31;
+    hf = lane >> 5;
+    // K operand: row li (+ 32 kt), 16-byte chunk hf (+ 2 s), rows RSK chunks apart.
+    klo = (li * FlashBf16Cfg<E>::RSK + hf) * 16;
+    // V^T operand (as v_operand): lane (j, dh, hf) reads the 4-element run of
+    // row 4 hf + j / 4 at column 16 dh + 4 (j % 4).
+    const int j = lane & 15, dh = (lane >> 4) & 1;
+    vlo = ((4 * hf + (j >> 2)) * FlashBf16Cfg<E>::RSV * 8 + 16 * dh + 4 * (j & 3)) * 2;
+  }
+
+  // The Q loads of both column blocks (VGPRs; moved to AGPRs by q_home).
+  __device__ __forceinline__ void issue_q(const Bf16Pass& a) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int rb = r0 + 32 * cb;
+      const __amdgpu_buffer_rsrc_t rs = tile_rsrc(a.q + (int64_t)rb * a.qs1, ((int64_t)(a.L - 1 - rb) * a.qs1 + E) * 2);
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        qr[cb][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (li * a.qs1 + 16 * s + 8 * hf) * 2, 0, 0));
+    }
+  }
+
+  // Q to the AGPRs, O = 0 (written by MFMAs, so the accumulators are born in
+  // AGPRs), and the softmax state reset.
+  __device__ __forceinline__ void q_home() {
+    const bf16x8 z = bf16x8{};
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) asm("" : "+a"(qr[cb][s]));
+#pragma unroll
+      for (int d = 0; d < ND; ++d) asm("v_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(o[cb][d]) : "v"(z));
+      m[cb] = -INFINITY;
+      nmu[cb] = 0.f;
+      l[cb] = 0.f;
+    }
+  }
+
+  // LDS byte address of buf + off, opaque to the compiler's reassociation.
+  __device__ __forceinline__ static uint32_t lds_base(const uint16_t* buf, int off) {
+    uint32_t a = (uint32_t)reinterpret_cast<uintptr_t>((const lds_void*)buf) + off;
+    asm volatile("" : "+v"(a));
+    return a;
+  }
+
+  // At least 11 wait states (an 8-pass MFMA) before a VALU read of an MFMA result.
+  __device__ __forceinline__ static void mfma_guard() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Keys of tile t row (cb, li) may see: key 32kt + 8(r/4) + 4hf + r%4 of the
+  // tile is visible when 32kt + 8(r/4) + r%4 <= the returned limit.
+  __device__ __forceinline__ int vis_of(const Bf16Pass& a, int t, int cb) const {
+    const int k0 = t * BN;
+    int lim = a.S - 1 - k0;
+    if (a.causal) lim = min(lim, r0 + 32 * cb + li + a.diag - k0);
+    return max(-1, min(lim, BN)) - 4 * hf;
+  }
+
+  // The MFMAs and the pins below are volatile so that they keep their order and
+  // their slot in the stream (the compiler would otherwise move pure arithmetic
+  // freely across the slots).
+  __device__ __forceinline__ void mfma_pv(int cb, int d, const bf16x8& vop, const bf16x8& p) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(o[cb][d]) : "v"(vop), "v"(p));
+  }
+
+  template <int PAR>
+  __device__ __forceinline__ void mfma_s(int cb, int kt, int s, const bf16x8& kop) {
+    if (s == 0)
+      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(st[PAR][cb][kt]) : "v"(kop), "a"(qr[cb][s]));
+    else
+      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(st[PAR][cb][kt]) : "v"(kop), "a"(qr[cb][s]));
+  }
+
+  // -inf for the keys of st[PAR] past each row's limit (tile t), in place.
+  template <int PAR>
+  __device__ __forceinline__ void apply_mask(const Bf16Pass& a, int t) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int vis = vis_of(a, t, cb);
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          st[PAR][cb][kt][r] = mask_key(st[PAR][cb][kt][r], vis, 32 * kt + 8 * (r >> 2) + (r & 3));
+    }
+  }
+
+  // Fixes each row's max at tile 0's (every row that sees any key sees key 0),
+  // in scaled log2 units as the reference takes it.
+  __device__ __forceinline__ void fix_max(float c) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[0][cb][kt][r]);
+      m[cb] = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+      nmu[cb] = m[cb] == -INFINITY ? 0.f : -m[cb];
+    }
+  }
+
+  // Iteration t of the walk, as one stream in which every MFMA shares its issue
+  // slot with VALU work:
+  //   PV:   O^T += V^T P^T for tile t-1 (V^T from vb, P^T from pb);
+  //   SN:   S^T = K Q^T for tile t+1 (K from kb) into st[PAR ^ 1];
+  //   SOFT: the softmax of tile t from st[PAR] (masked beforehand where the
+  //         tile needs it) into new P^T, rounded to bf16 as the reference's
+  //         bf16 policy does (flash_vec.mojo:255-259; l sums the unrounded p).
+  // `loads` (this wave's share of the next tiles' loads) goes out after the
+  // first operand reads.  Returns false when a row's sum of p over the tile
+  // exceeds the fast walk's headroom (or is NaN).
+  // PRE: the first NPRE operands (V^T, PV) were read by the previous iteration
+  // into opn.  NEXT: read the next iteration's first NPRE V^T operands from
+  // vnext into opn at the end (tile vnext has landed before this iteration's
+  // barrier, so they need not wait for it).
+  template <int PAR, bool PV, bool SN, bool SOFT, bool PRE = false, bool NEXT = false, typename F>
+  __device__ __forceinline__ bool step(const uint16_t* vb, const uint16_t* kb, float c, F&& loads,
+                                       const uint16_t* vnext = nullptr) {
+    constexpr float kHeadSum = 1048576.f;  // a lane's p summed over a tile <= 2^20
+    constexpr int NPVo = PV ? NPV : 0, NOP = NPVo + (SN ? NSK : 0), NM = 2 * NOP;
+    constexpr int NSLOT = NM > 0 ? NM : 1, NSC = SOFT ? 64 : 0;
+    static_assert(NSC % NSLOT == 0, "scores spread evenly over the MFMA slots");
+    // Operand addresses: one per-lane base per buffer, constant offsets.
+    // The bases are opaque to the compiler (it would otherwise fold the constant
+    // offsets into per-operand base registers, kept live across the loop, and
+    // add the buffer's offset to each of them).
+    const uint32_t vbase = lds_base(vb, vlo), kbase = lds_base(kb, klo);
+    auto read_v = [&](uint32_t base, int q) __attribute__((always_inline)) {
+      const int cc = q / ND, d = q % ND;
+      bf16x4v h[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        h[u] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (lds_bf16x4*)(uintptr_t)(base + ((16 * cc + 8 * u) * FlashBf16Cfg<E>::RSV * 8 + 32 * d) * 2));
+      return bf16x8{h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
+    };
+    auto read = [&](int q) __attribute__((always_inline)) {
+      if (q < NPVo) return read_v(vbase, q);
+      const int j = q - NPVo, kt = j & 1, sq = j >> 1;
+      return *(lds_bf16x8*)(uintptr_t)(kbase + (32 * kt * FlashBf16Cfg<E>::RSK + 2 * sq) * 16);
+    };
+    static_assert(!PRE || PV, "operands read ahead are V^T operands");
+    bf16x8 op[NOP > 0 ? NOP : 1];
+#pragma unroll
+    for (int q = 0; q < (NOP < LA ? NOP : LA); ++q) op[q] = (PRE && q < NPRE) ? opn[q] : read(q);
+    loads();
+    __builtin_amdgcn_sched_barrier(0);
+    // Score x (in the order of the P^T groups (cc, cb), so that the P^T of a
+    // group is complete early; the P.V MFMAs read the previous P^T) goes through
+    // three stages in consecutive slots: the exponent (slot of x), exp2 (next
+    // slot), the row sum and the bf16 pair (the one after), so that no stage
+    // waits in its slot for the result of the stage before it.
+    constexpr int PER = NSC / NSLOT;
+    float ls[2] = {0.f, 0.f};
+    float sv[64], ev[64];
+    uint32_t pw[2][4][4];
+    auto coords = [](int x, int& cb, int& cc, int& kt, int& r, int& jj) __attribute__((always_inline)) {
+      const int g = x >> 3;
+      jj = x & 7;
+      cb = g & 1;
+      cc = g >> 1;
+      kt = cc >> 1;
+      r = 8 * (cc & 1) + jj;
+    };
+#pragma unroll
+    for (int i = 0; i < NSLOT + (SOFT ? 2 : 0); ++i) {
+      // The slot's VALU work goes first: it overlaps the previous slot's MFMA
+      // and gives the operand read of this slot's MFMA more time.
+      // Each stage is one fixed-order assembly block (volatile: the blocks keep
+      // their slots).  Spacing kept by the stage order: an exp2 result is read
+      // two slots later, an exponent one slot later, and the register an exp2
+      // reads is not rewritten by the instruction right after it.
+      if (i >= 2) {  // stage 3 for the scores of slot i - 2: row sums, bf16 pairs
+#pragma unroll
+        for (int x = (i - 2) * PER; x < (i - 1) * PER; ++x) {
+          int cb, cc, kt, r, jj;
+          coords(x, cb, cc, kt, r, jj);
+          if (jj & 1)
+            asm volatile("v_add_f32 %0, %0, %2\n\tv_cvt_pk_bf16_f32 %1, %3, %2"
+                         : "+v"(ls[cb]), "=&v"(pw[cb][cc][jj >> 1])
+                         : "v"(ev[x]), "v"(ev[x - 1]));
+          else
+            asm volatile("v_add_f32 %0, %0, %1" : "+v"(ls[cb]) : "v"(ev[x]));
+        }
+      }
+      if (i < NSLOT) {  // stage 1 for the scores of slot i: exponents s*c - m
+#pragma unroll
+        for (int x = i * PER; x < (i + 1) * PER; ++x) {
+          int cb, cc, kt, r, jj;
+          coords(x, cb, cc, kt, r, jj);
+          asm volatile("v_fma_f32 %0, %1, %2, %3" : "=&v"(sv[x]) : "v"(st[PAR][cb][kt][r]), "s"(c), "v"(nmu[cb]));
+        }
+      }
+      if (i >= 1 && i <= NSLOT) {  // stage 2 for the scores of slot i - 1: exp2
+#pragma unroll
+        for (int x = (i - 1) * PER; x < i * PER; ++x) asm volatile("v_exp_f32 %0, %1" : "=&v"(ev[x]) : "v"(sv[x]));
+      }
+      if ((i & 1) == 0 && i / 2 + LA < NOP) op[i / 2 + LA] = read(i / 2 + LA);
+      if (i < NM) {
+        const int q = i >> 1, cb = i & 1;
+        if (q < NPVo) {
+          mfma_pv(cb, q % ND, op[q], pb[cb][q / ND]);
+        } else {
+          const int j = q - NPVo;
+          mfma_s<PAR ^ 1>(cb, j & 1, j >> 1, op[q]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (NEXT) {
+      const uint32_t nbase = lds_base(vnext, vlo);
+#pragma unroll
+      for (int q = 0; q < NPRE; ++q) opn[q] = read_v(nbase, q);
+    }
+    if (!SOFT) return true;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+        pb[cb][cc] = __builtin_bit_cast(bf16x8, u32x4{pw[cb][cc][0], pw[cb][cc][1], pw[cb][cc][2], pw[cb][cc][3]});
+    l[0] += ls[0];
+    l[1] += ls[1];
+    return ls[0] <= kHeadSum && ls[1] <= kHeadSum;
+  }
+
+  // out = acc / l per column block; a row with no visible key is 0.
+  __device__ __forceinline__ void store(const Bf16Pass& a) {
+    mfma_guard();
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const float lt = l[cb] + __shfl_xor(l[cb], 32);
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      const int row = r0 + 32 * cb + li;
+      if (row < a.L) {
+        uint16_t* orow = a.out + (int64_t)row * a.heads * E;
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            u32x2 w = {pack_bf16x2(o[cb][d][4 * q] * inv, o[cb][d][4 * q + 1] * inv),
+                       pack_bf16x2(o[cb][d][4 * q + 2] * inv, o[cb][d][4 * q + 3] * inv)};
+            *reinterpret_cast<u32x2*>(orow + 32 * d + 8 * q + 4 * hf) = w;
+          }
+      }
+    }
+  }
+};
+
+// The safe pass of the 64-row kernel: both column blocks of every wave walk the
+// pass with a lazily refreshed running max (as bf16_safe_pass), one tile buffer
+// each for K and V, loaded by all 4 waves.  Waves with `active` false compute and
+// store nothing but take part in the loads and barriers.
+template <int E>
+__device__ __noinline__ void bf16_safe_pass_p64(const Bf16Pass& a, bool active) {
+  using C = FlashP64Cfg<E>;
+  constexpr int BN = C::BN, ND = E / 32, NL = C::NL;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* Ks = smem;
+  uint16_t* Vs = smem + C::NBUF * C::TBUF;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int koff[NL], voff[NL];
+  tile_offsets<E, FlashBf16Cfg<E>::RSK>(wv, lane, a.ks1, koff);
+  tile_offsets<E, FlashBf16Cfg<E>::RSV>(wv, lane, a.vs1, voff);
+  TileStream<E> tk, tv;
+  tk.init(a.k, a.ks1, a.kend, Ks, 1, 0, wv);
+  tv.init(a.v, a.vs1, a.kend, Vs, 1, 0, wv);
+  const int nkt = a.kend > 0 ? (a.kend + BN - 1) / BN : 0;
+  Bf16Rows<E> w[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    w[cb].lane = lane;
+    w[cb].li = lane & 31;
+    w[cb].hf = lane >> 5;
+    w[cb].r0 = a.q0 + 64 * wv + 32 * cb;
+    w[cb].load_q(a);
+  }
+  __syncthreads();  // the fast walk is done with the tile buffers
+  for (int t = 0; t < nkt; ++t) {
+    tk.issue(koff);
+    tv.issue(voff);
+    loads_done_barrier();
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int kend_w = a.causal ? min(a.S, w[cb].r0 + 32 + a.diag) : a.S;
+      const int nkt_w = active && kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
+      if (t < nkt_w) {
+        f32x16 st[2];
+        w[cb].logits(Ks, st);
+        const int vis = w[cb].vis_of(a, t);
+        const float mt = w[cb].tile_max(st, vis, a.c);
+        if (__any(mt > w[cb].m + 8.f)) {
+          const float mn = fmaxf(w[cb].m, mt);
+          const float alpha = __builtin_amdgcn_exp2f(w[cb].m - (mn == -INFINITY ? 0.f : mn));
+          w[cb].l *= alpha;
+#pragma unroll
+          for (int d = 0; d < ND; ++d) w[cb].o[d] *= alpha;
+          w[cb].m = mn;
+        }
+        bf16x8 pb[4];
+        w[cb].template softmax<true>(st, vis, a.c, pb);
+        w[cb].pv(Vs, pb);
+      }
+    }
+    __syncthreads();  // every wave is done with the tiles before they are refilled
+  }
+  if (active) {
+    w[0].store(a);
+    w[1].store(a);
+  }
+}
+
+template <int E>
+__global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
+  using C = FlashP64Cfg<E>;
+  constexpr int BM = C::BM, BN = C::BN, NL = C::NL;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* Ks = smem;                      // K tile buffers [NBUF]
+  uint16_t* Vs = smem + C::NBUF * C::TBUF;  // V tile buffers [NBUF]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const PairWork pw = pair_work(p, BM);
+  // Positions and token strides fit 32 bits (the launcher declines otherwise).
+  Bf16Pass a;
+  a.L = (int)p.seq_q;
+  a.S = (int)p.seq_k;
+  a.diag = a.S - a.L;
+  a.qs1 = (int)p.qs[1];
+  a.ks1 = (int)p.ks[1];
+  a.vs1 = (int)p.vs[1];
+  a.heads = (int)p.heads;
+  a.c = p.c;
+  a.causal = p.causal;
+  a.q = reinterpret_cast<const uint16_t*>(p.q) + pw.b * p.qs[0] + pw.h * p.qs[2];
+  a.k = reinterpret_cast<const uint16_t*>(p.k) + pw.b * p.ks[0] + pw.h * p.ks[2];
+  a.v = reinterpret_cast<const uint16_t*>(p.v) + pw.b * p.vs[0] + pw.h * p.vs[2];
+  a.out = reinterpret_cast<uint16_t*>(p.out) + (pw.b * p.seq_q * p.heads + pw.h) * E;
+  const int S = a.S, diag = a.diag;
+  int koff[NL], voff[NL];
+  tile_offsets<E, FlashBf16Cfg<E>::RSK>(wv, lane, a.ks1, koff);
+  tile_offsets<E, FlashBf16Cfg<E>::RSV>(wv, lane, a.vs1, voff);
+
+  P64Rows<E> w;
+  w.init(lane);
+  auto kbuf = [&](int t) { return Ks + (t % C::NBUF) * C::TBUF; };
+  auto vbuf = [&](int t) { return Vs + (t % C::NBUF) * C::TBUF; };
+
+  for (int pass = 0; pass < pw.n; ++pass) {
+    const int q0 = (int)(pass == 0 ? pw.qb0 : pw.qb1) * BM;
+    w.r0 = q0 + 64 * wv;
+    const int kend_b = p.causal ? min(S, q0 + BM + diag) : S;
+    const int nkt = kend_b > 0 ? (kend_b + BN - 1) / BN : 0;
+    const int kend_w = p.causal ? min(S, w.r0 + 64 + diag) : S;
+    const int nkt_w = kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
+    a.q0 = q0;
+    a.kend = kend_b;
+
+    if (pass > 0) __syncthreads();  // every wave is done with the previous pass's tiles
+    w.issue_q(a);
+    // The walk.  K(j) lives in buffer j % 3 and is read by iteration j - 1 (the
+    // S of tile j); V(j) lives in buffer j % 3 and is read by iteration j + 1
+    // (the P.V of tile j).  Iteration t issues K(t+3) (into the buffer of K(t),
+    // last read at t-1) and V(t+1) (into that of V(t-2), last read at t-1), and
+    // ends with a block barrier after each wave has waited for all but those
+    // loads, so K(t+2) and V(t) have landed for iteration t+1.
+    TileStream<E> tk, tv;
+    tk.init(a.k, a.ks1, kend_b, Ks, C::NBUF, 0, wv);
+    tv.init(a.v, a.vs1, kend_b, Vs, C::NBUF, 0, wv);
+    if (nkt > 0) {
+      tk.issue(koff);
+      tk.issue(koff);
+      tk.issue(koff);
+      tv.issue(voff);
+    }
+    w.q_home();
+    bool bad = false;
+    if (nkt > 0) {
+      loads_landed_barrier<2 * NL>();  // K(0) and K(1) have landed
+      auto loads = [&]() __attribute__((always_inline)) {
+        tk.issue(koff);
+        tv.issue(voff);
+      };
+      // A tile needs the key limits when a row of the wave ends inside it.
+      auto masked = [&](int t) __attribute__((always_inline)) {
+        const int k0 = t * BN;
+        return k0 + BN > S || (p.causal && k0 + BN - 1 > w.r0 + diag);
+      };
+      int t = 0;
+      if (nkt_w > 0) {
+        // Tile 0: its S, the row max fixed at its own (never refreshed: the sum
+        // of a lane's p over a tile stays below 2^20 unless a later logit
+        // exceeds the fixed max by about 20 in log2 units, which `bad` records
+        // for the safe pass), then the softmax of tile 0 beside the S of tile 1.
+        w.template step<1, false, true, false>(Vs, kbuf(0), a.c, [] {});
+        P64Rows<E>::mfma_guard();
+        w.template apply_mask<0>(a, 0);
+        w.fix_max(a.c);
+        bad |= !w.template step<0, false, true, true, false, true>(Vs, kbuf(1), a.c, loads, vbuf(0));
+        loads_landed_barrier<2 * NL>();
+        // Tiles 1 .. nkt_w - 1: the P.V of the previous tile, the softmax of
+        // this one and the S of the next (past the wave's last tile that S is
+        // of a tile it does not use).
+        auto body = [&](auto par_tag, int tt) __attribute__((always_inline)) {
+          constexpr int PAR = decltype(par_tag)::value;
+          if (masked(tt)) w.template apply_mask<PAR>(a, tt);
+          bad |= !w.template step<PAR, true, true, true, true, true>(vbuf(tt + C::NBUF - 1), kbuf(tt + 1), a.c, loads,
+                                                                   vbuf(tt));
+          loads_landed_barrier<2 * NL>();
+        };
+        for (t = 1; t + 1 < nkt_w; t += 2) {
+          body(std::integral_constant<int, 1>{}, t);
+          body(std::integral_constant<int, 0>{}, t + 1);
+        }
+        if (t < nkt_w) {
+          body(std::integral_constant<int, 1>{}, t);
+          ++t;
+        }
+        // t == nkt_w: the P.V of the last tile.
+        w.template step<0, true, false, false, true>(vbuf(t + C::NBUF - 1), Ks, a.c, loads);
+        loads_landed_barrier<2 * NL>();
+        ++t;
+      }
+      // Tiles of the block past this wave's rows: loads and barriers only.
+      for (; t <= nkt; ++t) {
+        loads();
+        loads_landed_barrier<2 * NL>();
+      }
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads past the range (zeros) have landed
+    }
+    bad = __any(bad);
+    if (!bad) w.store(a);
+    if (__syncthreads_or(bad)) bf16_safe_pass_p64<E>(a, bad);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fp32
 // ---------------------------------------------------------------------------
 template <int E>
@@ -909,9 +1403,15 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
     const int64_t nqb = cdiv(p.seq_q, FlashBf16Cfg<128>::BM);
     const int64_t nb = p.batch * p.heads * (p.causal ? (nqb + 1) / 2 : nqb);
     switch (E) {
+#if CA_FLASH_P64
+      case 32: return launch_lds(flash_bf16_p64_kernel<32>, nb, 64 * FlashP64Cfg<32>::NW, FlashP64Cfg<32>::LDS_BYTES, p, stream);
+      case 64: return launch_lds(flash_bf16_p64_kernel<64>, nb, 64 * FlashP64Cfg<64>::NW, FlashP64Cfg<64>::LDS_BYTES, p, stream);
+      case 128: return launch_lds(flash_bf16_p64_kernel<128>, nb, 64 * FlashP64Cfg<128>::NW, FlashP64Cfg<128>::LDS_BYTES, p, stream);
+#else
       case 32: return launch_lds(flash_bf16_kernel<32>, nb, 64 * FlashBf16Cfg<32>::NW, FlashBf16Cfg<32>::LDS_BYTES, p, stream);
       case 64: return launch_lds(flash_bf16_kernel<64>, nb, 64 * FlashBf16Cfg<64>::NW, FlashBf16Cfg<64>::LDS_BYTES, p, stream);
       case 128: return launch_lds(flash_bf16_kernel<128>, nb, 64 * FlashBf16Cfg<128>::NW, FlashBf16Cfg<128>::LDS_BYTES, p, stream);
+#endif
     }
   } else {
     const int64_t nb = p.batch * p.heads * cdiv(p.seq_q, kBM);
