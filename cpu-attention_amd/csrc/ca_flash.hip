@@ -741,9 +741,11 @@ struct FlashP64Cfg {
   static constexpr int BN = FlashBf16Cfg<E>::BN;
   static constexpr int NL = FlashBf16Cfg<E>::NL;  // direct loads per wave and tile (K or V)
   static constexpr int TBUF = FlashBf16Cfg<E>::TBUF;
-  static constexpr int NBUF = 3;
-  static constexpr int LDS_BYTES = NBUF * 2 * TBUF * 2;
+  static constexpr int NBUFK = 4;  // K tiles: K(t+3) goes out while S(t+1) reads K(t+1)
+  static constexpr int NBUFV = 3;  // V tiles: V(t+1) goes out while P.V reads V(t-1)
+  static constexpr int LDS_BYTES = (NBUFK + NBUFV) * TBUF * 2;
   static_assert(NW == FlashBf16Cfg<E>::NWG, "the tile loads are split over NWG waves");
+  static_assert(LDS_BYTES + 1024 <= 160 * 1024, "tile buffers fit the LDS with room for the block's own");
 };
 
 // 64 query rows of one (batch, head) as two 32-row column blocks cb: lane (query
@@ -754,12 +756,10 @@ struct P64Rows {
   static constexpr int NPV = 4 * ND;  // V^T operands of a tile: keys 16cc.., dims 32d..
   static constexpr int NSK = 2 * NS;  // K operands of a tile: keys 32kt.., dims 16s..
   static constexpr int LA = 6;        // operand reads run LA operands ahead of their MFMAs
-  static constexpr int NPRE = LA < NPV ? LA : NPV;  // V^T operands read ahead across a barrier
   bf16x8 qr[2][NS];    // Q^T of column block cb as B operands (AGPRs)
   f32x16 o[2][ND];     // O^T accumulators (AGPRs): dims 32d + 8(r/4) + 4hf + r%4
   f32x16 st[2][2][2];  // S^T of two consecutive tiles: [tile parity][cb][kt]
   bf16x8 pb[2][4];     // P^T of the latest softmax: [cb][16-key group cc]
-  bf16x8 opn[NPRE];    // the next iteration's first V^T operands, read before the barrier
   float m[2], nmu[2], l[2];
   int li, hf, lane, r0;
   int klo, vlo;  // this lane's byte offsets of its K and V^T operand reads in a tile buffer
@@ -881,13 +881,8 @@ struct P64Rows {
   // `loads` (this wave's share of the next tiles' loads) goes out after the
   // first operand reads.  Returns false when a row's sum of p over the tile
   // exceeds the fast walk's headroom (or is NaN).
-  // PRE: the first NPRE operands (V^T, PV) were read by the previous iteration
-  // into opn.  NEXT: read the next iteration's first NPRE V^T operands from
-  // vnext into opn at the end (tile vnext has landed before this iteration's
-  // barrier, so they need not wait for it).
-  template <int PAR, bool PV, bool SN, bool SOFT, bool PRE = false, bool NEXT = false, typename F>
-  __device__ __forceinline__ bool step(const uint16_t* vb, const uint16_t* kb, float c, F&& loads,
-                                       const uint16_t* vnext = nullptr) {
+  template <int PAR, bool PV, bool SN, bool SOFT, typename F>
+  __device__ __forceinline__ bool step(const uint16_t* vb, const uint16_t* kb, float c, F&& loads) {
     constexpr float kHeadSum = 1048576.f;  // a lane's p summed over a tile <= 2^20
     constexpr int NPVo = PV ? NPV : 0, NOP = NPVo + (SN ? NSK : 0), NM = 2 * NOP;
     constexpr int NSLOT = NM > 0 ? NM : 1, NSC = SOFT ? 64 : 0;
@@ -911,10 +906,9 @@ struct P64Rows {
       const int j = q - NPVo, kt = j & 1, sq = j >> 1;
       return *(lds_bf16x8*)(uintptr_t)(kbase + (32 * kt * FlashBf16Cfg<E>::RSK + 2 * sq) * 16);
     };
-    static_assert(!PRE || PV, "operands read ahead are V^T operands");
     bf16x8 op[NOP > 0 ? NOP : 1];
 #pragma unroll
-    for (int q = 0; q < (NOP < LA ? NOP : LA); ++q) op[q] = (PRE && q < NPRE) ? opn[q] : read(q);
+    for (int q = 0; q < (NOP < LA ? NOP : LA); ++q) op[q] = read(q);
     loads();
     __builtin_amdgcn_sched_barrier(0);
     // Score x (in the order of the P^T groups (cc, cb), so that the P^T of a
@@ -979,11 +973,6 @@ struct P64Rows {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (NEXT) {
-      const uint32_t nbase = lds_base(vnext, vlo);
-#pragma unroll
-      for (int q = 0; q < NPRE; ++q) opn[q] = read_v(nbase, q);
-    }
     if (!SOFT) return true;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
@@ -1028,7 +1017,7 @@ __device__ __noinline__ void bf16_safe_pass_p64(const Bf16Pass& a, bool active) 
   constexpr int BN = C::BN, ND = E / 32, NL = C::NL;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   uint16_t* Ks = smem;
-  uint16_t* Vs = smem + C::NBUF * C::TBUF;
+  uint16_t* Vs = smem + C::NBUFK * C::TBUF;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   int koff[NL], voff[NL];
@@ -1087,8 +1076,8 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
   using C = FlashP64Cfg<E>;
   constexpr int BM = C::BM, BN = C::BN, NL = C::NL;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* Ks = smem;                      // K tile buffers [NBUF]
-  uint16_t* Vs = smem + C::NBUF * C::TBUF;  // V tile buffers [NBUF]
+  uint16_t* Ks = smem;                       // K tile buffers [NBUFK]
+  uint16_t* Vs = smem + C::NBUFK * C::TBUF;  // V tile buffers [NBUFV]
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -1115,8 +1104,8 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
 
   P64Rows<E> w;
   w.init(lane);
-  auto kbuf = [&](int t) { return Ks + (t % C::NBUF) * C::TBUF; };
-  auto vbuf = [&](int t) { return Vs + (t % C::NBUF) * C::TBUF; };
+  auto kbuf = [&](int t) { return Ks + (t % C::NBUFK) * C::TBUF; };
+  auto vbuf = [&](int t) { return Vs + (t % C::NBUFV) * C::TBUF; };
 
   for (int pass = 0; pass < pw.n; ++pass) {
     const int q0 = (int)(pass == 0 ? pw.qb0 : pw.qb1) * BM;
@@ -1130,15 +1119,19 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
 
     if (pass > 0) __syncthreads();  // every wave is done with the previous pass's tiles
     w.issue_q(a);
-    // The walk.  K(j) lives in buffer j % 3 and is read by iteration j - 1 (the
-    // S of tile j); V(j) lives in buffer j % 3 and is read by iteration j + 1
-    // (the P.V of tile j).  Iteration t issues K(t+3) (into the buffer of K(t),
-    // last read at t-1) and V(t+1) (into that of V(t-2), last read at t-1), and
-    // ends with a block barrier after each wave has waited for all but those
-    // loads, so K(t+2) and V(t) have landed for iteration t+1.
+    // The walk.  K(j) lives in buffer j % 4 and is read by iteration j - 1 (the
+    // S of tile j; K(0) by the pass's first S, before iteration 0); V(j) lives
+    // in buffer j % 3 and is read by iteration j + 1 (the P.V of tile j).
+    // Iteration t issues K(t+3) (into the buffer of K(t-1), last read at t-2)
+    // and V(t+1) (into that of V(t-2), last read at t-1), and ends with a block
+    // barrier after each wave has waited for all but those loads, so K(t+2) and
+    // V(t) have landed when iteration t+1 starts.  Every buffer a load refills
+    // was last read before a barrier that the load comes after, whichever wave
+    // issues it, and every tile is read only after a barrier that follows its
+    // landing.
     TileStream<E> tk, tv;
-    tk.init(a.k, a.ks1, kend_b, Ks, C::NBUF, 0, wv);
-    tv.init(a.v, a.vs1, kend_b, Vs, C::NBUF, 0, wv);
+    tk.init(a.k, a.ks1, kend_b, Ks, C::NBUFK, 0, wv);
+    tv.init(a.v, a.vs1, kend_b, Vs, C::NBUFV, 0, wv);
     if (nkt > 0) {
       tk.issue(koff);
       tk.issue(koff);
@@ -1168,7 +1161,7 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
         P64Rows<E>::mfma_guard();
         w.template apply_mask<0>(a, 0);
         w.fix_max(a.c);
-        bad |= !w.template step<0, false, true, true, false, true>(Vs, kbuf(1), a.c, loads, vbuf(0));
+        bad |= !w.template step<0, false, true, true>(Vs, kbuf(1), a.c, loads);
         loads_landed_barrier<2 * NL>();
         // Tiles 1 .. nkt_w - 1: the P.V of the previous tile, the softmax of
         // this one and the S of the next (past the wave's last tile that S is
@@ -1176,8 +1169,7 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
         auto body = [&](auto par_tag, int tt) __attribute__((always_inline)) {
           constexpr int PAR = decltype(par_tag)::value;
           if (masked(tt)) w.template apply_mask<PAR>(a, tt);
-          bad |= !w.template step<PAR, true, true, true, true, true>(vbuf(tt + C::NBUF - 1), kbuf(tt + 1), a.c, loads,
-                                                                   vbuf(tt));
+          bad |= !w.template step<PAR, true, true, true>(vbuf(tt + C::NBUFV - 1), kbuf(tt + 1), a.c, loads);
           loads_landed_barrier<2 * NL>();
         };
         for (t = 1; t + 1 < nkt_w; t += 2) {
@@ -1189,7 +1181,7 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
           ++t;
         }
         // t == nkt_w: the P.V of the last tile.
-        w.template step<0, true, false, false, true>(vbuf(t + C::NBUF - 1), Ks, a.c, loads);
+        w.template step<0, true, false, false>(vbuf(t + C::NBUFV - 1), Ks, a.c, loads);
         loads_landed_barrier<2 * NL>();
         ++t;
       }

@@ -64,6 +64,18 @@ def test_repeated_calls_follow_changes(cuda):
         run(1, s, s, 4, 64, torch.float32, causal, seed=s, device=cuda, scale=scale)
 
 
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_waves_without_rows_leave_tiles_alone(cuda, d):
+    """Causal calls with far fewer keys than queries: in a block, waves whose rows
+    see no key only issue their share of the tile loads and wait at the barriers
+    while the others read the tiles.  A load of theirs that refilled a buffer
+    still being read (the pass's first K tile, a V tile read before its barrier)
+    corrupted a few rows now and then; repeated calls must all hold."""
+    for rep in range(6):
+        run(2, 850, 86, 1, d, torch.bfloat16, True, seed=23 + rep, device=cuda)
+        run(1, 700, 70, 4, d, torch.bfloat16, True, seed=7 + rep, device=cuda)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_rows_without_keys_are_zero(cuda, dtype):
     """Causal with seq_q > seq_k: the first seq_q - seq_k rows see no key and are 0."""
