@@ -54,7 +54,7 @@ COPY_BYTES = 1 << 30  # the calibration copy of --profile-pass
 TRAFFIC = {
     "copy": {"fetch_kib": 524307.7, "write_kib": 1048576.0},
     "decode": {"fetch_kib": 543466.4, "write_kib": 512.0},
-    "prefill": {"fetch_kib": 325223.0, "write_kib": 174080.0},
+    "prefill": {"fetch_kib": 306997.6, "write_kib": 152967.2},
 }
 
 
@@ -269,7 +269,7 @@ def main():
             "us_per_call": round(pcall * 1e3, 1), "us_per_call_median": round(float(np.median(pms)) * 1e3, 1),
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
-                         "traffic": traffic_bytes("prefill"), "kernel": "flash_bf16_kernel<128>",
+                         "traffic": traffic_bytes("prefill"), "kernel": "flash_bf16_p64_kernel<128>",
                          "algorithmic_flop": flop},
         }
         del qkv, q, k, v
