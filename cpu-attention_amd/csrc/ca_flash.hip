@@ -984,24 +984,38 @@ struct P64Rows {
     return ls[0] <= kHeadSum && ls[1] <= kHeadSum;
   }
 
-  // out = acc / l per column block; a row with no visible key is 0.
-  __device__ __forceinline__ void store(const Bf16Pass& a) {
+  // Bytes of LDS that store_staged needs per wave: 32 rows of E bf16, padded.
+  static constexpr int kStageRow = 2 * E + 16;
+  static constexpr int kStageBytes = 32 * kStageRow;
+
+  // out = acc / l, staged through this wave's `stage` area of LDS one column
+  // block at a time: in the O^T layout a lane holds 4-dim runs of one row, so
+  // direct stores would touch 32 rows per instruction; staged, each store
+  // instruction writes whole rows (64 / (E/8) rows of E/8 16-byte chunks).  The
+  // area is private to the wave, whose LDS accesses run in order.  A row with no
+  // visible key is 0.
+  __device__ __forceinline__ void store_staged(const Bf16Pass& a, char* stage) {
+    constexpr int CPR = E / 8, RPI = 64 / CPR;  // 16-byte chunks per row, rows per store
     mfma_guard();
+    const int ch = lane % CPR, rr0 = lane / CPR;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const float lt = l[cb] + __shfl_xor(l[cb], 32);
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
-      const int row = r0 + 32 * cb + li;
-      if (row < a.L) {
-        uint16_t* orow = a.out + (int64_t)row * a.heads * E;
+      char* rowp = stage + li * kStageRow;
 #pragma unroll
-        for (int d = 0; d < ND; ++d)
+      for (int d = 0; d < ND; ++d)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            u32x2 w = {pack_bf16x2(o[cb][d][4 * q] * inv, o[cb][d][4 * q + 1] * inv),
-                       pack_bf16x2(o[cb][d][4 * q + 2] * inv, o[cb][d][4 * q + 3] * inv)};
-            *reinterpret_cast<u32x2*>(orow + 32 * d + 8 * q + 4 * hf) = w;
-          }
+        for (int q = 0; q < 4; ++q) {
+          u32x2 v = {pack_bf16x2(o[cb][d][4 * q] * inv, o[cb][d][4 * q + 1] * inv),
+                     pack_bf16x2(o[cb][d][4 * q + 2] * inv, o[cb][d][4 * q + 3] * inv)};
+          *reinterpret_cast<u32x2*>(rowp + (32 * d + 8 * q + 4 * hf) * 2) = v;
+        }
+#pragma unroll
+      for (int k = 0; k < 32 / RPI; ++k) {
+        const int rr = rr0 + RPI * k, row = r0 + 32 * cb + rr;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stage + rr * kStageRow + ch * 16);
+        if (row < a.L) *reinterpret_cast<u32x4*>(a.out + (int64_t)row * a.heads * E + ch * 8) = v;
       }
     }
   }
@@ -1192,9 +1206,13 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
       }
       __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads past the range (zeros) have landed
     }
+    // After the barrier every wave's tile loads have landed and nobody reads the
+    // tiles any more: the tile buffers can stage the output.
     bad = __any(bad);
-    if (!bad) w.store(a);
-    if (__syncthreads_or(bad)) bf16_safe_pass_p64<E>(a, bad);
+    const bool any_bad = __syncthreads_or(bad);
+    static_assert(C::NW * P64Rows<E>::kStageBytes <= C::LDS_BYTES, "the staging areas fit the tile buffers");
+    if (!bad) w.store_staged(a, reinterpret_cast<char*>(smem) + wv * P64Rows<E>::kStageBytes);
+    if (any_bad) bf16_safe_pass_p64<E>(a, bad);
   }
 }
 
