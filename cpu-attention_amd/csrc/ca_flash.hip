@@ -5,11 +5,12 @@
 // tiles past the last visible key are never touched, the online softmax runs in
 // base 2 with c = scale*log2(e), and a row that sees no key is exactly 0.
 //
-// bf16 (flash_bf16_kernel): 8 waves x 32 query rows per block, one block per CU,
-// so each SIMD runs two waves, which take turns between MFMA work and softmax
-// work (ping-pong; a wave's own VALU and MFMA work do not overlap).  Key tiles
-// of 64 go global -> LDS with direct buffer loads two tiles ahead; K is read
-// with ds_read_b128, V^T with ds_read_b64_tr_b16 from the row-major V tile.
+// bf16 (flash_bf16_p64_kernel, the default): 4 waves x 64 query rows per block,
+// one wave per SIMD.  A wave's VALU work runs while its own independent MFMAs
+// execute, so each wave issues one stream per key tile of 64: the P.V MFMAs of
+// the previous tile, the S MFMAs of the next and the softmax of this one.  Key
+// tiles go global -> LDS with direct buffer loads; K is read with ds_read_b128,
+// V^T with ds_read_b64_tr_b16 from the row-major V tile.
 //   S^T = K Q^T   32x32x16 MFMAs with keys as rows and queries as columns, so a
 //                 lane ends up owning one query and 16 keys of each 32-key half;
 //   softmax       per lane (its query) against a max fixed at the first tile;
@@ -18,6 +19,9 @@
 //   O^T += V^T P^T the probabilities are already in the B-operand layout of the
 //                 MFMA (no LDS round trip); P is rounded to bf16 as the reference's
 //                 bf16 policy does (flash_vec.mojo:255-259), fp32 accumulation.
+// bf16 (flash_bf16_kernel, built with CA_FLASH_P64=0): its predecessor, 8 waves x
+// 32 rows, two waves per SIMD taking turns between an MFMA phase and a softmax
+// phase.
 // fp32 (flash_f32_kernel): 4 waves x 32 rows, K/V staged through registers into
 // LDS, v_mfma_f32_32x32x2_f32, everything fp32.
 #include <type_traits>
