@@ -824,11 +824,15 @@ struct P64Rows {
 
   // Keys of tile t row (cb, li) may see: key 32kt + 8(r/4) + 4hf + r%4 of the
   // tile is visible when 32kt + 8(r/4) + r%4 <= the returned limit.
+  // The lane id is recomputed here (this runs only on masked tiles), so that no
+  // register holds a lane constant for it across the walk.
   __device__ __forceinline__ int vis_of(const Bf16Pass& a, int t, int cb) const {
+    int lid;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lid));
     const int k0 = t * BN;
     int lim = a.S - 1 - k0;
-    if (a.causal) lim = min(lim, r0 + 32 * cb + li + a.diag - k0);
-    return max(-1, min(lim, BN)) - 4 * hf;
+    if (a.causal) lim = min(lim, r0 + 32 * cb + (lid & 31) + a.diag - k0);
+    return max(-1, min(lim, BN)) - 4 * (lid >> 5);
   }
 
   // The MFMAs and the pins below are volatile so that they keep their order and
@@ -846,7 +850,9 @@ struct P64Rows {
       asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(st[PAR][cb][kt]) : "v"(kop), "a"(qr[cb][s]));
   }
 
-  // -inf for the keys of st[PAR] past each row's limit (tile t), in place.
+  // -inf for the keys of st[PAR] past each row's limit (tile t), in place: one
+  // fixed assembly block per logit with a single temporary (the compiler would
+  // interleave the elements and run out of registers on this rare path).
   template <int PAR>
   __device__ __forceinline__ void apply_mask(const Bf16Pass& a, int t) {
 #pragma unroll
@@ -855,8 +861,14 @@ struct P64Rows {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          st[PAR][cb][kt][r] = mask_key(st[PAR][cb][kt][r], vis, 32 * kt + 8 * (r >> 2) + (r & 3));
+        for (int r = 0; r < 16; ++r) {
+          int tmp;
+          asm volatile(
+              "v_subrev_u32 %1, %3, %2\n\tv_ashrrev_i32 %1, 31, %1\n\t"
+              "v_and_b32 %1, 0xff800000, %1\n\tv_add_f32 %0, %0, %1"
+              : "+v"(st[PAR][cb][kt][r]), "=&v"(tmp)
+              : "v"(vis), "i"(32 * kt + 8 * (r >> 2) + (r & 3)));
+        }
     }
   }
 
