@@ -54,7 +54,7 @@ COPY_BYTES = 1 << 30  # the calibration copy of --profile-pass
 TRAFFIC = {
     "copy": {"fetch_kib": 524307.7, "write_kib": 1048576.0},
     "decode": {"fetch_kib": 543466.4, "write_kib": 512.0},
-    "prefill": {"fetch_kib": 317539.6, "write_kib": 157696.0},
+    "prefill": {"fetch_kib": 312573.0, "write_kib": 152576.0},
 }
 
 
