@@ -480,15 +480,29 @@ def llc_bytes():
     return 32 << 20
 
 
-_WS = threading.local()
+_WS = {}
+_WS_LOCK = threading.Lock()
 
 
 def workspace(nbytes=0):
-    """This thread's flash workspace on the current GPU as (address, bytes), grown
-    to ``nbytes`` and never shrunk; (0, 0) until something asks for one."""
-    ws = getattr(_WS, "t", None)
-    if nbytes and (ws is None or ws.numel() < nbytes or ws.device.index != torch.cuda.current_device()):
-        _WS.t = ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
-    if ws is None:
+    """A flash workspace for callers of ``module().flash`` that pass their own, as
+    (address, bytes): one per (thread, device, current stream), grown to
+    ``nbytes`` and never shrunk; (0, 0) until something asks for one.
+
+    Keyed by stream because calls on two streams would otherwise write the same
+    partials at once.  A buffer that is outgrown is kept (not returned to the
+    allocator) until the process ends, since a captured graph may still name its
+    address.  The package's own ``flash_attn_func`` does not use this: it
+    allocates the scratch per call on the current stream."""
+    if not torch.cuda.is_available():
         return 0, 0
-    return ws.data_ptr(), ws.numel()
+    dev = torch.cuda.current_device()
+    key = (threading.get_ident(), dev, _stream(torch.device("cuda", dev)))
+    with _WS_LOCK:
+        held = _WS.setdefault(key, [])
+        if nbytes and (not held or held[-1].numel() < nbytes):
+            size = max(nbytes, 2 * held[-1].numel()) if held else nbytes
+            held.append(torch.empty(size, dtype=torch.uint8, device=f"cuda:{dev}"))
+        if not held:
+            return 0, 0
+        return held[-1].data_ptr(), held[-1].numel()

@@ -140,8 +140,14 @@ def flash_attn_with_kvcache(
         if out is not None:
             return out
         # Positions outside the page table get slot -1 (not stored) instead of an
-        # out-of-range gather; the decode below then reports the overflow.
+        # out-of-range gather.  With host checks on, a prompt that does not fit is
+        # refused before any of it is written (the reference's gather fails
+        # before its store does).
         n, page = k.shape[1], k_cache.shape[2]
+        if K.host_checks() and isinstance(cache_seqlens, torch.Tensor) and cache_seqlens.numel() \
+                and isinstance(page_table, torch.Tensor) and page_table.dim() == 2 \
+                and int(cache_seqlens.max()) + n > page_table.shape[1] * page:
+            raise ValueError("cpu_attention: cache_seqlens exceed the page table's capacity")
         table = page_table.to(k.device).long()
         pos = cache_seqlens.to(k.device).long()[:, None] + torch.arange(n, device=k.device)[None]
         inside = (pos >= 0) & (pos < table.shape[1] * page)
@@ -231,11 +237,15 @@ def flash_attn_func(q, k, v, softmax_scale=None, causal=False):
 
 def _flash(q, k, v, softmax_scale, causal):
     rt, _, flash = _NATIVE or _native()
-    ws, nbytes = K.workspace()
-    out = flash(rt, q, k, v, softmax_scale, causal, ws, nbytes)
-    if type(out) is int:  # the workspace was short: grow it once
-        ws, nbytes = K.workspace(out)
-        out = flash(rt, q, k, v, softmax_scale, causal, ws, nbytes)
+    out = flash(rt, q, k, v, softmax_scale, causal, 0, 0)
+    if type(out) is int:
+        # The few-rows route asked for split-K scratch (an int = the bytes it
+        # needs).  It is allocated for this call on the current stream: the
+        # caching allocator hands the bytes to nothing else until the kernels
+        # queued on that stream have used them, and under graph capture the
+        # graph's own pool keeps them for every replay.
+        ws = torch.empty(out, dtype=torch.uint8, device=q.device)
+        out = flash(rt, q, k, v, softmax_scale, causal, ws.data_ptr(), ws.numel())
     return out
 
 

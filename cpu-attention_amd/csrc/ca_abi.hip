@@ -41,15 +41,18 @@ extern "C" int ca_store(const ca_store_args* a, void* stream) {
   if (a->num_tokens < 0 || a->num_heads <= 0 || a->num_blocks < 0) return CA_DECLINED;
   if (a->num_tokens == 0) return CA_OK;
   if (!a->key || !a->value || !a->k_cache || !a->v_cache || !a->slot_mapping) return CA_DECLINED;
-  if (!aligned16(a->key) || !aligned16(a->value) || !aligned16(a->k_cache) ||
-      !aligned16(a->v_cache) || !stride16(a->token_stride, a->dtype) ||
-      a->token_stride < a->num_heads * a->head_dim)
+  if (!aligned16(a->key) || !aligned16(a->value) || !aligned16(a->k_cache) || !aligned16(a->v_cache))
+    return CA_DECLINED;
+  // One token is never stepped over, so its stride is not read (a [1, H, E]
+  // view may carry any stride there, 0 included).
+  const bool one = a->num_tokens == 1;
+  if (!one && (!stride16(a->token_stride, a->dtype) || a->token_stride < a->num_heads * a->head_dim))
     return CA_DECLINED;
   const int64_t words = a->head_dim * esize(a->dtype) / 4;
   StoreParams p{};
   p.key = static_cast<const uint32_t*>(a->key);
   p.value = static_cast<const uint32_t*>(a->value);
-  p.tok_stride_w = a->token_stride * esize(a->dtype) / 4;
+  p.tok_stride_w = one ? 0 : a->token_stride * esize(a->dtype) / 4;
   p.kc = static_cast<uint32_t*>(a->k_cache);
   p.vc = static_cast<uint32_t*>(a->v_cache);
   p.slots = a->slot_mapping;

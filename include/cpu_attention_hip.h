@@ -57,7 +57,8 @@ enum { CA_OK = 0, CA_DECLINED = 1, CA_HIP_ERROR = -1 };
 typedef struct ca_store_args {
   const void* key;
   const void* value;
-  int64_t token_stride;  /* elements between consecutive tokens of key/value */
+  int64_t token_stride;  /* elements between consecutive tokens of key/value
+                            (not read when num_tokens == 1) */
   void* k_cache;
   void* v_cache;
   const int64_t* slot_mapping;  /* [num_tokens], int64 */

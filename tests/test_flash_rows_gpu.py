@@ -4,9 +4,7 @@ dim and dtype, key lengths at and past the chunk edges (one chunk, several, a
 partial last one), single rows and row groups of 4 with a partial last group,
 causal rows that see no key, strided q/k/v views, the boundary with the tiled
 route, the cross shape of the BASELINE prefill config, and the workspace
-protocol (the first call of a thread finds the workspace short and retries)."""
-
-import threading
+protocol (the entry reports the bytes it needs; the API allocates them per call)."""
 
 import numpy as np
 import pytest
@@ -77,23 +75,38 @@ def test_cfg4_cross_shape_rows(cuda):
     run(8, 1, 2048, 32, 32, torch.bfloat16, False, seed=12, device=cuda)
 
 
-def test_workspace_grows_in_a_new_thread(cuda):
-    """A fresh thread has no workspace: the first call finds it short, grows it
-    and retries (the reference's flash_attn_interface.py:186-193 protocol)."""
-    errs = []
+def test_few_rows_calls_on_two_streams(cuda):
+    """Split-K calls queued on two streams at once, each with its own scratch: the
+    partials of one never land in the other's (a scratch shared per thread
+    would race here)."""
+    b, sq, sk, h, d = 2, 2, 3000, 8, 64
+    g = torch.Generator().manual_seed(21)
+    cases = [tuple(torch.randn(b, n, h, d, generator=g).bfloat16().to(cuda) for n in (sq, sk, sk))
+             for _ in range(2)]
+    streams = [torch.cuda.Stream(device=cuda) for _ in range(2)]
+    torch.cuda.synchronize()
+    outs = []
+    for _ in range(4):
+        for (q, k, v), st in zip(cases, streams):
+            with torch.cuda.stream(st):
+                outs.append(flash_attn_func(q, k, v, causal=False))
+    torch.cuda.synchronize()
+    for i, out in enumerate(outs):
+        q, k, v = cases[i % 2]
+        assert_close(out, attention(values(q), values(k), values(v), d ** -0.5), torch.bfloat16, paged=False)
 
-    def work():
-        try:
-            assert K.workspace() == (0, 0)
-            run(2, 2, 3000, 8, 64, torch.bfloat16, False, seed=21, device=cuda)
-            assert K.workspace()[1] > 0
-        except Exception as e:  # noqa: BLE001 - reported below
-            errs.append(e)
 
-    t = threading.Thread(target=work)
-    t.start()
-    t.join()
-    assert not errs, errs
+def test_engine_workspace_per_stream(cuda):
+    """``K.workspace()`` (for callers of the module entry) keeps one buffer per
+    stream and grows it only upward."""
+    a = K.workspace(1000)
+    assert a[1] >= 1000 and K.workspace() == a
+    st = torch.cuda.Stream(device=cuda)
+    with torch.cuda.stream(st):
+        assert K.workspace() == (0, 0)
+        b = K.workspace(10)
+        assert b[0] != a[0]
+    assert K.workspace(10) == a
 
 
 def test_native_entry_reports_the_workspace_it_needs(cuda):

@@ -154,16 +154,22 @@ def test_prompt_append_replays(cuda, dtype, no_host_checks):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("sq,sk", [(300, 300), (3, 3000)])
 def test_flash_attn_func_replays(cuda, dtype, sq, sk):
-    """Prefill: the tiled route and the few-rows route, whose split-K workspace the
-    warm-up calls before the capture have already grown."""
+    """Prefill: the tiled route and the few-rows route, whose split-K scratch is
+    allocated inside the capture from the graph's own pool."""
     b, h, d = 2, 4, 64
     q, k, v = (torch.zeros(b, n, h, d, dtype=dtype, device=cuda) for n in (sq, sk, sk))
     graph, out = capture(lambda: flash_attn_func(q, k, v, causal=True))
     g = torch.Generator(device=cuda).manual_seed(9)
-    for _ in range(3):
+    for i in range(3):
         for t in (q, k, v):
             t.copy_(torch.randn(t.shape, generator=g, device=cuda).to(dtype))
         ref = flash_attn_func(q.clone(), k.clone(), v.clone(), causal=True)
+        if i == 1:
+            # A larger eager call between replays (more scratch than the captured
+            # one): the graph keeps its own scratch, so the replay is unaffected.
+            big = torch.randn(b, sq, h, d, generator=g, device=cuda).to(dtype)
+            bigk = torch.randn(b, 4 * sk, h, d, generator=g, device=cuda).to(dtype)
+            flash_attn_func(big, bigk, bigk, causal=True)
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()

@@ -159,6 +159,51 @@ def test_store_bit_exact(cuda, dtype, d, page, pattern):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("source", ["contiguous", "fused_view", "module_entry"])
+def test_store_one_token(cuda, dtype, source):
+    """One token (a batch-1 serving step): reshape_and_cache and the module's store
+    entry, from a contiguous [1, H, E] tensor and from a one-token view of a fused
+    projection, byte-equal to the layout oracle."""
+    h, d, page, nb = 4, 128, 16, 5
+    g = torch.Generator().manual_seed(3)
+    fused = torch.randn(1, 3 * h * d, generator=g).to(dtype).to(cuda)
+    if source == "fused_view":
+        key, value = fused[:, :h * d].view(1, h, d), fused[:, 2 * h * d:].view(1, h, d)
+    else:
+        key, value = (torch.randn(1, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))
+    slots = torch.tensor([2 * page + 7], dtype=torch.int64)
+    kc = torch.full((nb, h, page, d), float("nan"), dtype=dtype, device=cuda)
+    vc = kc.clone()
+    if source == "module_entry":
+        assert K.module().store(K.runtime(), key, value, kc, vc, slots.to(cuda)) is True
+    else:
+        reshape_and_cache(key, value, kc, vc, slots.to(cuda))
+    kw = cache_words(torch.full((nb, h, page, d), float("nan"), dtype=dtype))
+    vw = kw.copy()
+    layout.store(kw, vw, row_words(key), row_words(value), slots.numpy(), page)
+    np.testing.assert_array_equal(cache_words(kc), kw)
+    np.testing.assert_array_equal(cache_words(vc), vw)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_cache_batch_idx(cuda, dtype):
+    """``cache_batch_idx`` picks the page-table row of each query
+    (flash_attn_interface.py:103-104): here queries attend the staged sequences in
+    another order, one of them twice."""
+    lens, h, d, page = [40, 3, 77], 4, 64, 16
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=17, device=cuda)
+    idx = torch.tensor([2, 0, 2, 1])
+    g = torch.Generator().manual_seed(4)
+    q4 = torch.randn(4, 1, h, d, generator=g).to(dtype).to(cuda)
+    seqlens = torch.tensor([lens[i] for i in idx], dtype=torch.int32, device=cuda)
+    for where in (cuda, "cpu"):
+        out = flash_attn_with_kvcache(q4, kc, vc, cache_seqlens=seqlens, page_table=bt,
+                                      cache_batch_idx=idx.to(where))
+        ref = reference(q4, [ks[i] for i in idx], [vs[i] for i in idx], d ** -0.5)
+        assert_close(out, ref, dtype, paged=True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_multi_token_append_bytes(cuda, dtype):
     """The multi-token append (flash_attn_interface.py:109-117) writes what the
     layout oracle's prompt slots say, then decodes over the grown cache."""
@@ -325,7 +370,7 @@ def test_prompt_append_strided_and_cpu_lengths(cuda):
 
 def test_prompt_append_past_the_page_table(cuda):
     """More new tokens than the page table holds: with host checks the reference's
-    ValueError; without them no fault, the tokens that fit are stored and the
+    ValueError, raised before any token is written; without them no fault, the tokens that fit are stored and the
     row attends the table's capacity."""
     h, d, page = 2, 64, 16
     table = torch.tensor([[0, 1]], dtype=torch.int32, device=cuda)
@@ -337,10 +382,10 @@ def test_prompt_append_past_the_page_table(cuda):
         flash_attn_with_kvcache(q, kc, vc, k=k, v=k, cache_seqlens=torch.tensor([0], dtype=torch.int32,
                                                                                 device=cuda),
                                 page_table=table)
+    torch.cuda.synchronize()
+    assert not kc.any() and not vc.any(), "a refused prompt wrote part of itself"
     old = K.set_host_checks(False)
     try:
-        kc.zero_()
-        vc.zero_()
         out = K.module().append_decode(K.runtime(), q, kc, vc, k, k, torch.tensor([0], dtype=torch.int32,
                                                                                    device=cuda), table, None)
         assert out is not None and torch.isfinite(out).all()
