@@ -32,11 +32,11 @@ DTYPES = {torch.float32: 0, torch.bfloat16: 1}
 HEAD_DIMS = (32, 64, 128)
 _DIR = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = "libcpu_attention_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 _ESIZE = {torch.float32: 4, torch.bfloat16: 2}
 _PLAIN = (torch.Tensor, torch.nn.Parameter)
 
-CA_OK, CA_DECLINED = 0, 1
+CA_OK, CA_DECLINED, CA_SCRATCH_EXCEEDED = 0, 1, 2
 
 
 class StoreArgs(ctypes.Structure):
@@ -80,7 +80,7 @@ class FlashArgs(ctypes.Structure):
     ]
 
 
-EXPORTS = ("ca_store", "ca_decode", "ca_decode_workspace_bytes", "ca_flash",
+EXPORTS = ("ca_store", "ca_decode", "ca_decode_noalloc", "ca_decode_workspace_bytes", "ca_flash",
            "ca_flash_workspace_bytes", "ca_abi_version", "ca_version", "ca_status_string")
 
 _HOST_CHECKS = [os.environ.get("CPU_ATTENTION_HOST_CHECKS", "1") != "0"]
@@ -111,6 +111,8 @@ def load_library(path=None):
     lib.ca_store.restype = ctypes.c_int
     lib.ca_decode.argtypes = [ctypes.POINTER(DecodeArgs), vp]
     lib.ca_decode.restype = ctypes.c_int
+    lib.ca_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), vp]
+    lib.ca_decode_noalloc.restype = ctypes.c_int
     lib.ca_decode_workspace_bytes.argtypes = [i64, i64, i64, i64, i64]
     lib.ca_decode_workspace_bytes.restype = i64
     lib.ca_flash.argtypes = [ctypes.POINTER(FlashArgs), vp]

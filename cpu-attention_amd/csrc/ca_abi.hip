@@ -25,12 +25,15 @@ bool page_ok(int64_t page) { return page > 0 && page % 16 == 0; }
 extern "C" int ca_abi_version(void) { return CA_ABI_VERSION; }
 
 extern "C" const char* ca_version(void) {
-  return "cpu-attention gfx950 (MI355X) HIP kernels, ABI " "2";
+  return "cpu-attention gfx950 (MI355X) HIP kernels, ABI " "3";
 }
 
 extern "C" const char* ca_status_string(int status) {
   if (status == CA_OK) return "ok";
   if (status == CA_DECLINED) return "declined: arguments outside what the kernels take";
+  if (status == CA_SCRATCH_EXCEEDED)
+    return "ca_decode_noalloc: the call needs more split-K scratch than the fixed 32 MiB buffer "
+           "(a page table of this capacity needs ca_decode with a caller workspace)";
   if (status < 0) return hipGetErrorString((hipError_t)(CA_HIP_ERROR - status));
   return "unknown status";
 }
@@ -146,6 +149,23 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
   p.part_ml = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + acc_bytes);
   p.out = a->out;
   return decode_launch(p, (int)a->head_dim, a->dtype == CA_BF16, st);
+}
+
+extern "C" int ca_decode_noalloc(const ca_decode_args* a, void* stream) {
+  static_assert(CA_DECODE_NOALLOC_SCRATCH_BYTES == (32ll << 20), "the status string names the size");
+  if (!a) return CA_DECLINED;
+  const int64_t need = ca_decode_workspace_bytes(a->num_seqs, a->num_heads, a->head_dim, a->page_size,
+                                                 a->page_table_width);
+  if (need > CA_DECODE_NOALLOC_SCRATCH_BYTES) return CA_SCRATCH_EXCEEDED;
+  ca_decode_args b = *a;
+  b.workspace = nullptr;
+  b.workspace_bytes = 0;
+  if (need > 0) {
+    const int r = decode_noalloc_scratch(&b.workspace);
+    if (r != CA_OK) return r;
+    b.workspace_bytes = CA_DECODE_NOALLOC_SCRATCH_BYTES;
+  }
+  return ca_decode(&b, stream);
 }
 
 extern "C" int64_t ca_flash_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t num_heads,

@@ -68,6 +68,7 @@ int store_launch(const StoreParams& p, int words, hipStream_t stream);
 int64_t decode_tiles(int64_t pt_width, int64_t page);
 int64_t decode_workspace_slots(int64_t rows, int64_t tiles);
 int decode_launch(const DecodeParams& p, int head_dim, int bf16, hipStream_t stream);
+int decode_noalloc_scratch(void** ptr);
 int flash_launch(const FlashParams& p, int head_dim, int bf16, hipStream_t stream);
 int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, int head_dim,
                                    bool bf16);

@@ -17,8 +17,9 @@
  *                    operands to a readable layout and calls again;
  *   CA_HIP_ERROR (<0) a HIP launch error; ca_status_string() names it.
  *
- * The entries are re-entrant and keep no global mutable state.  None allocates:
- * outputs and split-K scratch are passed in by the caller.
+ * The entries are re-entrant and keep no global mutable state (ca_decode_noalloc
+ * aside: it uses one fixed scratch buffer per GPU).  None allocates: outputs and
+ * split-K scratch are passed in by the caller.
  *
  * Data-dependent bounds (a slot past the cache's end, a length beyond the page
  * table's capacity, a page-table entry that names no block) are guarded inside
@@ -43,11 +44,13 @@
 extern "C" {
 #endif
 
-#define CA_ABI_VERSION 2
+#define CA_ABI_VERSION 3
 
 enum { CA_F32 = 0, CA_BF16 = 1 };
 
-enum { CA_OK = 0, CA_DECLINED = 1, CA_HIP_ERROR = -1 };
+/* CA_SCRATCH_EXCEEDED: ca_decode_noalloc only -- the call needs more split-K
+ * scratch than the library's fixed buffer holds; nothing was enqueued. */
+enum { CA_OK = 0, CA_DECLINED = 1, CA_SCRATCH_EXCEEDED = 2, CA_HIP_ERROR = -1 };
 
 /* reshape_and_cache (cpu_attention/cache.py:13-25, native entry `store`
  * cpu_attention/_mojo/src/_C.mojo:174-213).  Token i of key/value
@@ -128,6 +131,25 @@ typedef struct ca_decode_args {
 int64_t ca_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t head_dim,
                                   int64_t page_size, int64_t page_table_width);
 int ca_decode(const ca_decode_args* args, void* stream);
+
+/* ca_decode without a workspace argument and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory at call time (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as ca_decode;
+ * args->workspace and args->workspace_bytes are ignored.  The split-K scratch
+ * is a fixed device array inside the library, CA_DECODE_NOALLOC_SCRATCH_BYTES
+ * (32 MiB) per GPU, held from the first call on that GPU until the process
+ * ends; its address is resolved once per device (the current device at the
+ * call; `stream` must belong to it).  A call whose
+ * ca_decode_workspace_bytes(...) exceeds that size returns CA_SCRATCH_EXCEEDED
+ * and enqueues nothing (32 MiB covers, e.g., 4096 rows of E=128 up to 30,720
+ * keys of page-table capacity; rows of up to 2048 keys need none).  Every call
+ * on a GPU shares that GPU's one buffer: calls that overlap on one GPU (two
+ * streams, or two host threads) race on it and must be serialised by the
+ * caller.  The buffer needs no clearing: each call writes every partial it
+ * reads before reading it. */
+#define CA_DECODE_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int ca_decode_noalloc(const ca_decode_args* args, void* stream);
 
 /* Dense prefill (flash_attn_interface.py:168-193, native entry `flash`
  * _C.mojo:232-316).  q [batch, seq_q, H, E], k/v [batch, seq_k, H, E] with any

@@ -33,10 +33,11 @@ def test_library_exports_every_declared_entry():
 
 def test_version_and_status_strings():
     lib = K.load_library()
-    assert lib.ca_abi_version() == K.ABI_VERSION == 2
+    assert lib.ca_abi_version() == K.ABI_VERSION == 3
     assert b"gfx950" in lib.ca_version()
     assert lib.ca_status_string(0) == b"ok"
     assert b"declined" in lib.ca_status_string(1)
+    assert b"32 MiB" in lib.ca_status_string(K.CA_SCRATCH_EXCEEDED)
     assert lib.ca_status_string(-1 - 1)  # a HIP error code renders as text
 
 
@@ -89,6 +90,15 @@ def test_entries_decline_malformed_calls_without_a_gpu():
     assert lib.ca_decode(ctypes.byref(d), None) == K.CA_DECLINED  # dtype
     d.dtype = 1
     assert lib.ca_decode(ctypes.byref(d), None) == K.CA_DECLINED  # null pointers
+    # the no-allocation decode: a call whose split-K scratch exceeds the fixed buffer
+    # is refused before anything is enqueued (no GPU needed to see it)
+    d.dtype, d.page_table_width = 1, 4033  # 4033 pages of 16 keys: 32 blocks per row
+    d.num_seqs, d.num_heads, d.head_dim = 64, 32, 128
+    need = lib.ca_decode_workspace_bytes(64, 32, 128, 16, 4033)
+    assert need > 32 << 20
+    assert lib.ca_decode_noalloc(ctypes.byref(d), None) == K.CA_SCRATCH_EXCEEDED
+    assert lib.ca_decode_workspace_bytes(64, 32, 128, 16, 3800) <= 32 << 20
+    assert lib.ca_decode_noalloc(None, None) == K.CA_DECLINED
     f = K.FlashArgs(batch=1, seq_q=0, seq_k=4, num_heads=1, head_dim=64, dtype=1)
     assert lib.ca_flash(ctypes.byref(f), None) == K.CA_DECLINED  # seq_q < 1
     f.seq_q = 4

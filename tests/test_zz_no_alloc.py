@@ -1,0 +1,73 @@
+"""ca_decode_noalloc (the decode entry that allocates nothing; its split-K scratch
+is a fixed per-GPU buffer inside the library) against ca_decode with a caller
+workspace, through the C ABI: two calls in a row, the second with a smaller
+batch and page table, each bit-equal to ca_decode's output and within the
+decode gates of the float64 oracle; a call past the buffer's size is refused
+without touching the output."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from cpu_attention import _kernel as K
+from helpers import assert_close, reference, stage
+
+pytestmark = pytest.mark.gpu
+
+
+def args_for(q, kc, vc, lens, table, out, ws=None):
+    b, h, d = q.shape[0], q.shape[2], q.shape[3]
+    return K.DecodeArgs(
+        q=q.data_ptr(), q_stride=q.stride(0), k_cache=kc.data_ptr(), v_cache=vc.data_ptr(),
+        k_new=None, v_new=None, kv_stride=0, slots=None, lens=lens.data_ptr(),
+        page_table=table.data_ptr(), page_table_width=table.shape[1], out=out.data_ptr(),
+        num_seqs=b, num_heads=h, head_dim=d, page_size=kc.shape[2], num_blocks=kc.shape[0],
+        scale=d ** -0.5, dtype=K.DTYPES[q.dtype],
+        workspace=ws.data_ptr() if ws is not None else None,
+        workspace_bytes=ws.numel() if ws is not None else 0, new_tokens=0)
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_noalloc_matches_decode_on_two_calls(cuda, dtype):
+    lib = K.module().lib
+    h, d, page = 4, 128, 16
+    # First call: rows up to 5000 keys (three blocks of 2048 keys, so the split-K
+    # scratch and the combine kernel are in use); second: fewer rows and a
+    # narrower page table, still past one block.
+    for lens, seed in (([5000, 2100, 100, 4095], 1), ([3000, 17], 2)):
+        print(f"noalloc dtype={dtype} lens={lens}", flush=True)
+        q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=seed, device=cuda)
+        seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
+        need = lib.ca_decode_workspace_bytes(len(lens), h, d, page, bt.shape[1])
+        assert 0 < need <= 32 << 20
+        ws = torch.empty(need, dtype=torch.uint8, device=cuda)
+        ref_out = torch.empty_like(q)
+        rc = lib.ca_decode(ctypes.byref(args_for(q, kc, vc, seqlens, bt, ref_out, ws)), stream())
+        assert rc == K.CA_OK, lib.ca_status_string(rc)
+        out = torch.full_like(q, float("nan"))
+        rc = lib.ca_decode_noalloc(ctypes.byref(args_for(q, kc, vc, seqlens, bt, out)), stream())
+        assert rc == K.CA_OK, lib.ca_status_string(rc)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.uint8), ref_out.view(torch.uint8))
+        assert_close(out, reference(q, ks, vs, d ** -0.5), dtype, paged=True)
+
+
+def test_noalloc_refuses_past_its_buffer(cuda):
+    lib = K.module().lib
+    n, h, d, page, width = 64, 32, 128, 16, 4033
+    assert lib.ca_decode_workspace_bytes(n, h, d, page, width) > 32 << 20
+    q = torch.randn(n, 1, h, d, device=cuda).bfloat16()
+    kc = torch.zeros(2, h, page, d, device=cuda, dtype=torch.bfloat16)
+    table = torch.zeros(n, width, dtype=torch.int32, device=cuda)
+    lens = torch.ones(n, dtype=torch.int32, device=cuda)
+    out = torch.full_like(q, 7.0)
+    rc = lib.ca_decode_noalloc(ctypes.byref(args_for(q, kc, kc, lens, table, out)), stream())
+    assert rc == K.CA_SCRATCH_EXCEEDED
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
