@@ -56,3 +56,15 @@ def test_json_line_carries_the_contract(cuda):
         assert 0 < roof["frac"] < 1 and roof["traffic"] > 0
         assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
     assert d["roofline"]["bound"] == "hbm" and d["prefill"]["roofline"]["bound"] == "mfma"
+    # the clock ramp runs before the W warm-up calls of each leg, and is reported
+    assert d["clock_ramp_calls"] > 0 and d["prefill"]["clock_ramp_calls"] > 0
+    # every other BASELINE config, with its work, timings and roofline fraction
+    cfgs = d["configs"]
+    assert set(cfgs) == {"cfg1", "cfg2", "cfg4_cross", "cfg5_store", "cfg5_step"}
+    for name, c in cfgs.items():
+        assert c["value"] > 0 and 0 < c["roofline"]["frac"] < 1, name
+        assert "algorithmic_bytes" in c or "algorithmic_flop" in c or "algorithmic_bytes_per_step" in c
+    for name in ("cfg1", "cfg2", "cfg4_cross", "cfg5_store"):
+        c = cfgs[name]
+        assert c["us_per_call"] > 0 and c["us_per_call_cold"] > 0 and c["api_us_per_call"] > 0, name
+    assert cfgs["cfg5_step"]["us_per_step"] > 0
