@@ -19,9 +19,6 @@
 //   O^T += V^T P^T the probabilities are already in the B-operand layout of the
 //                 MFMA (no LDS round trip); P is rounded to bf16 as the reference's
 //                 bf16 policy does (flash_vec.mojo:255-259), fp32 accumulation.
-// bf16 (flash_bf16_kernel, built with CA_FLASH_P64=0): its predecessor, 8 waves x
-// 32 rows, two waves per SIMD taking turns between an MFMA phase and a softmax
-// phase.
 // fp32 (flash_f32_kernel): 4 waves x 32 rows, K/V staged through registers into
 // LDS, v_mfma_f32_32x32x2_f32, everything fp32.
 #include <type_traits>
@@ -32,10 +29,6 @@
 namespace ca {
 
 constexpr int kBM = 128;  // fp32: query rows per block (4 waves x 32)
-
-#ifndef CA_FLASH_P64
-#define CA_FLASH_P64 1
-#endif
 
 // A raw buffer resource over [base, base + bytes): loads past `bytes` return 0.
 // The per-tile K/V loads rebase the resource at each tile, so their per-lane
@@ -67,16 +60,11 @@ __device__ __forceinline__ BlockWork block_work(const FlashParams& p) {
 }
 
 // ---------------------------------------------------------------------------
-// bf16
+// bf16: key-tile geometry
 // ---------------------------------------------------------------------------
-// Block = 8 waves x 32 query rows, one block per CU, i.e. two waves per SIMD:
-// a wave's own VALU work does not overlap its own MFMAs on CDNA4, so the
-// softmax of one wave runs while the other wave's MFMAs do.  Key tiles of 64
-// go from global memory straight into LDS (buffer loads with LDS as the
-// destination: no staging registers; rows past the block's key range fill with
-// zeros), three buffers deep.  The waves in their MFMA phase issue the loads
-// (group 0 the K tiles, group 1 the V tiles): their issue slots are idle while
-// the matrix pipe works, whereas the softmax phase is short of them.
+// Key tiles of 64 go from global memory straight into LDS (buffer loads with LDS
+// as the destination: no staging registers; rows past the block's key range
+// fill with zeros), split over the block's 4 waves.
 //
 // LDS layouts: rows of E bf16 padded to RSK (K) or RSV (V) 16-byte chunks, so
 // operand reads are conflict-free and every address is a per-lane base plus a
@@ -85,9 +73,7 @@ __device__ __forceinline__ BlockWork block_work(const FlashParams& p) {
 // block (4 keys of one dim).
 template <int E>
 struct FlashBf16Cfg {
-  static constexpr int NW = 8;             // waves per block
-  static constexpr int NWG = 4;            // waves per ping-pong group
-  static constexpr int BM = 32 * NW;       // query rows per block
+  static constexpr int NWG = 4;            // waves that share a tile's loads
   static constexpr int BN = 64;            // keys per tile
   static constexpr int CPR = E / 8;        // 16-byte chunks per row
   // Padded row strides in chunks.  K: 16 lanes reading one 16-byte column of 16
@@ -97,16 +83,14 @@ struct FlashBf16Cfg {
   // cover the 64 banks once.
   static constexpr int RSK = CPR + 1;
   static constexpr int RSV = CPR == 16 ? 20 : (CPR == 8 ? 12 : 4);
-  // Direct loads per thread and tile: a group's 4 waves load a tile, every
-  // load of a wave fills 64 consecutive chunks, so a tile buffer is NL rounds
-  // of 4 x 64 chunks.  K and V tiles take the same NL (the larger), so every
-  // wave issues the same number of loads per tile and one wait count serves all.
+  // Direct loads per thread and tile: the 4 waves load a tile, every load of a
+  // wave fills 64 consecutive chunks, so a tile buffer is NL rounds of 4 x 64
+  // chunks.  K and V tiles take the same NL (the larger), so every wave issues
+  // the same number of loads per tile and one wait count serves all.
   static constexpr int NLK = (BN * RSK + 64 * NWG - 1) / (64 * NWG);
   static constexpr int NLV = (BN * RSV + 64 * NWG - 1) / (64 * NWG);
   static constexpr int NL = NLK > NLV ? NLK : NLV;
   static constexpr int TBUF = NL * 64 * NWG * 8;  // elements per tile buffer
-  static constexpr int NBUF = 3;                  // K loads run two tiles ahead
-  static constexpr int LDS_BYTES = NBUF * 2 * TBUF * 2;
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -163,8 +147,7 @@ __device__ __forceinline__ void tile_offsets(int wv4, int lane, int stride, int 
   }
 }
 
-// One wave's share of the successive K tiles (group 0) or V tiles (group 1) of
-// a pass: rows [k0, k0 + BN) of the source per tile, cut at the pass's key
+// One wave's share of the successive K tiles or V tiles of a pass: rows [k0, k0 + BN) of the source per tile, cut at the pass's key
 // range (rows past it read as zeros, a tile past it touches no memory), into
 // `nbuf` rotating tile buffers.  Every field is wave-uniform and advances by an
 // add per tile, so a tile's loads cost a few scalar instructions.
@@ -261,9 +244,8 @@ __device__ __forceinline__ float mask_key(float v, int vis, int key) {
   return v + __int_as_float(msk & (int)0xff800000u);
 }
 
-// Per-wave state and the pieces of the key-tile step shared by the fast walk
-// and the safe pass: 32 query rows of one (batch, head), lane (query li, half
-// hf).
+// State and key-tile step of the safe pass (one column block): 32 query rows of
+// one (batch, head), lane (query li, half hf), with a running max.
 template <int E>
 struct Bf16Rows {
   static constexpr int BN = FlashBf16Cfg<E>::BN, NS = E / 16, ND = E / 32;
@@ -365,89 +347,6 @@ struct Bf16Rows {
         o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_operand<E>(vb, lane, cc, d), pb[cc], o[d], 0, 0, 0);
   }
 
-  // One MFMA phase of the ping-pong walk: O^T += V^T P^T for the previous tile
-  // (PV, from vb and pb) and S^T = K Q^T for the next one (S, from kb into st),
-  // as one stream of MFMAs whose LDS operand reads run LA operands ahead, in
-  // scheduling regions of 4 MFMAs.  The lookahead keeps the LDS latency off the
-  // MFMA pipe; the regions keep the compiler from hoisting every read (which
-  // would not fit in a wave's 256 registers).  `mid` (the wave's tile loads)
-  // runs first, in a region of its own: placed inside the stream it cost
-  // registers across the loop.
-  template <bool PV, bool S, typename F>
-  __device__ __forceinline__ void mfma_phase(const uint16_t* vb, const bf16x8 (&pb)[4], const uint16_t* kb,
-                                             f32x16 (&st)[2], F&& mid) {
-    constexpr int NPV = PV ? 4 * ND : 0, NS2 = S ? 2 * NS : 0, NOP = NPV + NS2, LA = 8, R = LA + 1;
-    mid();
-    __builtin_amdgcn_sched_barrier(0);
-    bf16x8 buf[R];
-    // Stream position i -> operation: P.V MFMAs (< NPV) and S MFMAs alternate
-    // while both remain, so the two transposed V reads of a P.V MFMA and the one
-    // K read of an S MFMA spread evenly over the phase (the V reads alone, back to
-    // back, would keep the LDS busy for as long as their MFMAs take).
-    auto op = [](int i) {
-      constexpr int both = 2 * (NPV < NS2 ? NPV : NS2);
-      if (i < both) return (i & 1) ? NPV + (i >> 1) : (i >> 1);
-      return (NPV > NS2 ? 0 : NPV) + both / 2 + (i - both);  // the rest of the longer kind
-    };
-    auto read = [&](int i) {
-      if (i < NPV) return v_operand<E>(vb, lane, i / ND, i % ND);
-      const int j = i - NPV;
-      return k_operand<E>(kb, 32 * (j & 1) + li, j >> 1, hf);
-    };
-#pragma unroll
-    for (int i = 0; i < NOP + LA; ++i) {
-      if (i < NOP) buf[i % R] = read(op(i));
-      const int k0 = i - LA;
-      if (k0 >= 0) {
-        const int k = op(k0);
-        if (k < NPV) {
-          o[k % ND] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(buf[k0 % R], pb[k / ND], o[k % ND], 0, 0, 0);
-        } else {
-          const int j = k - NPV, kt = j & 1, s = j >> 1;
-          st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(buf[k0 % R], qr[s], s == 0 ? f32x16{} : st[kt], 0, 0, 0);
-        }
-        if ((k0 & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  }
-
-  // Bytes of LDS that store_staged needs per wave: 16 rows of E bf16, padded.
-  static constexpr int kStageRow = 2 * E + 16;
-  static constexpr int kStageBytes = 16 * kStageRow;
-
-  // out = acc / l, staged through this wave's `stage` area of LDS.  In the O^T
-  // layout a lane holds 4-dim runs of one row, so direct stores would touch 32
-  // rows per instruction with 16 bytes each; staged, each store instruction
-  // writes whole rows (64 / (E/8) rows of E/8 16-byte chunks).  Two rounds of 16
-  // rows; the area is private to the wave, whose LDS accesses run in order.
-  // A row with no visible key is 0.
-  __device__ __forceinline__ void store_staged(const Bf16Pass& a, char* stage) const {
-    constexpr int CPR = E / 8, RPI = 64 / CPR;  // 16-byte chunks per row, rows per store
-    const float lt = l + __shfl_xor(l, 32);
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    const int ch = lane % CPR, rr0 = lane / CPR;
-#pragma unroll
-    for (int rnd = 0; rnd < 2; ++rnd) {
-      if ((li >> 4) == rnd) {
-        char* rowp = stage + (li & 15) * kStageRow;
-#pragma unroll
-        for (int d = 0; d < ND; ++d)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            u32x2 w = {pack_bf16x2(o[d][4 * q] * inv, o[d][4 * q + 1] * inv),
-                       pack_bf16x2(o[d][4 * q + 2] * inv, o[d][4 * q + 3] * inv)};
-            *reinterpret_cast<u32x2*>(rowp + (32 * d + 8 * q + 4 * hf) * 2) = w;
-          }
-      }
-#pragma unroll
-      for (int k = 0; k < 16 / RPI; ++k) {
-        const int rr = rr0 + RPI * k, row = r0 + 16 * rnd + rr;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stage + rr * kStageRow + ch * 16);
-        if (row < a.L) *reinterpret_cast<u32x4*>(a.out + (int64_t)row * a.heads * E + ch * 8) = v;
-      }
-    }
-  }
-
   // out = acc / l; a row with no visible key is 0.
   __device__ __forceinline__ void store(const Bf16Pass& a) const {
     const float lt = l + __shfl_xor(l, 32);
@@ -467,265 +366,10 @@ struct Bf16Rows {
   }
 };
 
-// The safe pass: a walk with a lazily refreshed running max (refreshed when a
-// tile max exceeds it by more than 8, the accumulators rescaled then; acc/l
-// cancels the choice of max).  Every wave of the block takes part in the loads
-// and barriers; waves with `active` false compute and store nothing.  Used for
-// the rows whose logits outgrew the fast walk's fixed max; it is kept out of
-// line so that its registers do not constrain the fast walk's.
-template <int E>
-__device__ __noinline__ void bf16_safe_pass(const Bf16Pass& a, bool active) {
-  using C = FlashBf16Cfg<E>;
-  constexpr int BN = C::BN, ND = E / 32;
-  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* Ks = smem;
-  uint16_t* Vs = smem + C::NBUF * C::TBUF;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wg = wv >> 2, wv4 = wv & 3;
-  Bf16Rows<E> w;
-  w.lane = lane;
-  w.li = lane & 31;
-  w.hf = lane >> 5;
-  w.r0 = a.q0 + 32 * wv;
-  // Group 0 loads the K tiles, group 1 the V tiles, each into one buffer.
-  int off[C::NL];
-  {
-    int koff[C::NL], voff[C::NL];
-    tile_offsets<E, C::RSK>(wv4, lane, a.ks1, koff);
-    tile_offsets<E, C::RSV>(wv4, lane, a.vs1, voff);
-#pragma unroll
-    for (int i = 0; i < C::NL; ++i) off[i] = wg ? voff[i] : koff[i];
-  }
-  TileStream<E> ts;
-  ts.init(wg ? a.v : a.k, wg ? a.vs1 : a.ks1, a.kend, wg ? Vs : Ks, 1, 0, wv4);
-  const int nkt = a.kend > 0 ? (a.kend + BN - 1) / BN : 0;
-  const int kend_w = a.causal ? min(a.S, w.r0 + 32 + a.diag) : a.S;
-  const int nkt_w = active && kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
-  w.load_q(a);
-
-  __syncthreads();  // the fast walk is done with the tile buffers
-  for (int t = 0; t < nkt; ++t) {
-    ts.issue(off);
-    loads_done_barrier();
-    if (t < nkt_w) {
-      f32x16 st[2];
-      w.logits(Ks, st);
-      const int vis = w.vis_of(a, t);
-      const float mt = w.tile_max(st, vis, a.c);
-      if (__any(mt > w.m + 8.f)) {
-        const float mn = fmaxf(w.m, mt);
-        const float alpha = __builtin_amdgcn_exp2f(w.m - (mn == -INFINITY ? 0.f : mn));
-        w.l *= alpha;
-#pragma unroll
-        for (int d = 0; d < ND; ++d) w.o[d] *= alpha;
-        w.m = mn;
-      }
-      bf16x8 pb[4];
-      w.template softmax<true>(st, vis, a.c, pb);
-      w.pv(Vs, pb);
-    }
-    __syncthreads();  // every wave is done with the tiles before they are refilled
-  }
-  if (active) w.store(a);
-}
-
-template <int E>
-__global__ __launch_bounds__(512, 2) void flash_bf16_kernel(FlashParams p) {
-  using C = FlashBf16Cfg<E>;
-  constexpr int BM = C::BM, BN = C::BN;
-  // Headroom of the fast walk's fixed max: a lane's p summed over a tile <= 2^20.
-  constexpr float kHeadSum = 1048576.f;
-  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* Ks = smem;                      // K tile buffers [NBUF]
-  uint16_t* Vs = smem + C::NBUF * C::TBUF;  // V tile buffers [NBUF]
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches and windows
-  const PairWork pw = pair_work(p, BM);
-  // Positions and token strides fit 32 bits (the launcher declines otherwise).
-  Bf16Pass a;
-  a.L = (int)p.seq_q;
-  a.S = (int)p.seq_k;
-  a.diag = a.S - a.L;
-  a.qs1 = (int)p.qs[1];
-  a.ks1 = (int)p.ks[1];
-  a.vs1 = (int)p.vs[1];
-  a.heads = (int)p.heads;
-  a.c = p.c;
-  a.causal = p.causal;
-  a.q = reinterpret_cast<const uint16_t*>(p.q) + pw.b * p.qs[0] + pw.h * p.qs[2];
-  a.k = reinterpret_cast<const uint16_t*>(p.k) + pw.b * p.ks[0] + pw.h * p.ks[2];
-  a.v = reinterpret_cast<const uint16_t*>(p.v) + pw.b * p.vs[0] + pw.h * p.vs[2];
-  a.out = reinterpret_cast<uint16_t*>(p.out) + (pw.b * p.seq_q * p.heads + pw.h) * E;
-  const int S = a.S, diag = a.diag;
-  // Ping-pong groups: waves 0-3 and 4-7.  Group 0 loads the K tiles, group 1
-  // the V tiles.
-  const int wg = wv >> 2, wv4 = wv & 3;
-  int off[C::NL];
-  {
-    int koff[C::NL], voff[C::NL];
-    tile_offsets<E, C::RSK>(wv4, lane, a.ks1, koff);
-    tile_offsets<E, C::RSV>(wv4, lane, a.vs1, voff);
-#pragma unroll
-    for (int i = 0; i < C::NL; ++i) off[i] = wg ? voff[i] : koff[i];
-  }
-
-  Bf16Rows<E> w;
-  w.lane = lane;
-  w.li = lane & 31;
-  w.hf = lane >> 5;
-
-  // A pass: query block qb (rows q0..q0+BM-1), key tiles up to kend_b for the
-  // block and kend_w for this wave.
-  struct Geo {
-    int q0, kend_b, nkt, nkt_w;
-  };
-  auto geo = [&](int pass) {
-    Geo g;
-    g.q0 = (int)(pass == 0 ? pw.qb0 : pw.qb1) * BM;
-    g.kend_b = p.causal ? min(S, g.q0 + BM + diag) : S;
-    g.nkt = g.kend_b > 0 ? (g.kend_b + BN - 1) / BN : 0;
-    const int kend_w = p.causal ? min(S, g.q0 + 32 * wv + 32 + diag) : S;
-    g.nkt_w = kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
-    return g;
-  };
-  TileStream<E> ts;
-  // The first tiles of a pass: K(j) goes to buffer j % 3; V(-1) (zeros: the
-  // P.V at t = 0 has p = 0, and 0 * a stale NaN would not be 0) to buffer 2,
-  // V(j) to buffer j % 3.  K buffer 2 and V buffer 1 stay free until the walk.
-  auto prologue = [&](const Geo& g) {
-    ts.init(wg ? a.v : a.k, wg ? a.vs1 : a.ks1, g.kend_b, wg ? Vs : Ks, C::NBUF, wg ? 2 : 0, wv4);
-    if (wg)
-      ts.issue_zeros(off);
-    else
-      ts.issue(off);
-    ts.issue(off);
-  };
-  // This wave's output staging area: in K buffer 2 (group 0) or V buffer 1
-  // (group 1), which the next pass's prologue leaves alone.
-  static_assert(C::NWG * Bf16Rows<E>::kStageBytes <= C::TBUF * 2, "staging fits a tile buffer");
-  char* stage = reinterpret_cast<char*>(wg ? Vs + C::TBUF : Ks + 2 * C::TBUF) + wv4 * Bf16Rows<E>::kStageBytes;
-
-  Geo g = geo(0);
-  a.q0 = g.q0;
-  a.kend = g.kend_b;
-  w.r0 = g.q0 + 32 * wv;
-  w.load_q(a);
-  if (g.nkt > 0) prologue(g);
-  uint32_t bad_passes = 0;  // bit p: this wave's rows of pass p need the safe pass
-  for (int pass = 0; pass < pw.n; ++pass) {
-    const int nkt = g.nkt, nkt_w = g.nkt_w;
-    bool bad = false;
-
-    // The fast walk.  The row max is fixed at tile 0's (every row that sees any
-    // key sees key 0) and never refreshed, so the loop touches the accumulators
-    // only through MFMAs; the sum of a lane's p over a tile stays below 2^20
-    // (so every p does) unless a later logit exceeds the fixed max by about 20
-    // (log2 units) or more, which `bad` records.
-    //
-    // Ping-pong: group 0 and group 1 share each SIMD and take turns, half a
-    // tile apart, between an MFMA phase (the S MFMAs of tile t and the P.V
-    // MFMAs of tile t-1) and a VALU phase (the softmax of tile t).  Group g runs
-    // its MFMA phase for tile t at half-step h = 2t + g and its softmax of tile t
-    // at h = 2t + g + 1, so K(t) is read at h = 2t, 2t+1 and V(t) at h = 2t+2,
-    // 2t+3.  Each MFMA phase issues the next tile of its group's stream: group 0
-    // K(t+2) at h = 2t (into the buffer of K(t-1), last read at h = 2t-1),
-    // group 1 V(t+1) at h = 2t+1 (into the buffer of V(t-2), last read at
-    // h = 2t-1).  A block barrier ends every odd h = 2t+1, after each wave has
-    // waited for all but its latest tile (K(t+1) and V(t), read from h = 2t+2
-    // on).  Between two such barriers the waves read only tiles that landed
-    // before the first and write only buffers whose readers all ran before it,
-    // so no barrier is needed at even h; the groups keep their alternation by
-    // themselves (one barrier per tile was measured 3 % faster than two).
-    if (nkt > 0) {
-      constexpr int NL = C::NL;  // direct loads per wave and tile
-      f32x16 st[2];
-      bf16x8 pb[4];
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc) pb[cc] = bf16x8{};
-      auto kbuf = [&](int t) { return Ks + (t % C::NBUF) * C::TBUF; };
-      auto vbuf = [&](int t) { return Vs + ((t + C::NBUF) % C::NBUF) * C::TBUF; };
-      loads_done_barrier();
-      auto next_tile = [&] { ts.issue(off); };
-      for (int h = 0; h < 2 * nkt + 2; ++h) {
-        if (((h + wg) & 1) == 0) {
-          const int t = (h - wg) >> 1;
-          // Phases at t = 0 (P.V with pb = 0 over the zero V buffer) and
-          // t = nkt_w (S of a tile it does not use) run the same code.
-          if (t <= nkt_w && nkt_w > 0) {
-            __builtin_amdgcn_s_setprio(1);
-            w.template mfma_phase<true, true>(vbuf(t - 1), pb, kbuf(t), st, next_tile);
-            __builtin_amdgcn_s_setprio(0);
-          } else {
-            next_tile();
-          }
-        } else {
-          const int t = (h - 1 - wg) >> 1;
-          if (t >= 0 && t < nkt_w) {
-            const int k0 = t * BN;
-            float ls;
-            if (t == 0 || k0 + BN > S || (p.causal && k0 + BN - 1 > w.r0 + diag)) {
-              const int vis = w.vis_of(a, t);
-              if (t == 0) w.m = w.tile_max(st, vis, a.c);
-              ls = w.template softmax<true>(st, vis, a.c, pb);
-            } else {
-              ls = w.template softmax<false>(st, BN, a.c, pb);
-            }
-            bad |= !(ls <= kHeadSum);  // also NaN
-          }
-        }
-        if (h & 1) loads_landed_barrier<NL>();
-      }
-      __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads past the range (zeros) have landed
-    }
-    __syncthreads();  // every wave's tile loads have landed: all buffers are free
-    bad = __any(bad);
-    // The next pass's Q and first tiles go out now, so that their latency
-    // overlaps this pass's output stores.
-    const bool more = pass + 1 < pw.n;
-    Geo gn = g;
-    if (more) {
-      gn = geo(pass + 1);
-      w.issue_q(a, gn.q0 + 32 * wv);
-      if (gn.nkt > 0) prologue(gn);
-    }
-    // A wave whose fast walk recorded an overflow risk leaves its rows to the
-    // safe pass, after the last pass.
-    if (bad)
-      bad_passes |= 1u << pass;
-    else
-      w.store_staged(a, stage);
-    if (more) {
-      g = gn;
-      a.q0 = g.q0;
-      a.kend = g.kend_b;
-      w.r0 = g.q0 + 32 * wv;
-      w.reset();
-    }
-  }
-  // Rare: rows whose logits outgrew the fast walk's fixed max, redone with a
-  // running max once every pass is through (no register of the walk lives
-  // across the out-of-line call).  Every wave takes part in the barriers.
-  if (__syncthreads_or(bad_passes != 0)) {
-    __builtin_amdgcn_s_waitcnt(0x0f70);
-    __syncthreads();
-    for (int pass = 0; pass < pw.n; ++pass) {
-      const Geo gp = geo(pass);
-      a.q0 = gp.q0;
-      a.kend = gp.kend_b;
-      const bool act = (bad_passes >> pass) & 1;
-      if (__syncthreads_or(act)) bf16_safe_pass<E>(a, act);
-      __syncthreads();
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // bf16, 64 query rows per wave, softmax overlapped with the MFMAs
 // ---------------------------------------------------------------------------
-// Block = 4 waves x 64 query rows (the same 256-row query blocks as
-// flash_bf16_kernel), one wave per SIMD with the whole register file: Q and the
+// Block = 4 waves x 64 query rows (256-row query blocks), one wave per SIMD with the whole register file: Q and the
 // O accumulators live in AGPRs (only MFMAs read them), S, P and the operands in
 // VGPRs.  A wave's VALU work runs while its own MFMAs execute (measured on
 // gfx950: 4 MFMAs and 64 independent VALU ops per iteration take as long as the
@@ -1426,18 +1070,12 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
   if (rows_route(p.seq_q, bf16 != 0)) return flash_rows_launch(p, E, bf16, stream);
   if (bf16) {
     // One block per (batch, head) and query-block pair (causal) or query block.
-    const int64_t nqb = cdiv(p.seq_q, FlashBf16Cfg<128>::BM);
+    const int64_t nqb = cdiv(p.seq_q, FlashP64Cfg<128>::BM);
     const int64_t nb = p.batch * p.heads * (p.causal ? (nqb + 1) / 2 : nqb);
     switch (E) {
-#if CA_FLASH_P64
       case 32: return launch_lds(flash_bf16_p64_kernel<32>, nb, 64 * FlashP64Cfg<32>::NW, FlashP64Cfg<32>::LDS_BYTES, p, stream);
       case 64: return launch_lds(flash_bf16_p64_kernel<64>, nb, 64 * FlashP64Cfg<64>::NW, FlashP64Cfg<64>::LDS_BYTES, p, stream);
       case 128: return launch_lds(flash_bf16_p64_kernel<128>, nb, 64 * FlashP64Cfg<128>::NW, FlashP64Cfg<128>::LDS_BYTES, p, stream);
-#else
-      case 32: return launch_lds(flash_bf16_kernel<32>, nb, 64 * FlashBf16Cfg<32>::NW, FlashBf16Cfg<32>::LDS_BYTES, p, stream);
-      case 64: return launch_lds(flash_bf16_kernel<64>, nb, 64 * FlashBf16Cfg<64>::NW, FlashBf16Cfg<64>::LDS_BYTES, p, stream);
-      case 128: return launch_lds(flash_bf16_kernel<128>, nb, 64 * FlashBf16Cfg<128>::NW, FlashBf16Cfg<128>::LDS_BYTES, p, stream);
-#endif
     }
   } else {
     const int64_t nb = p.batch * p.heads * cdiv(p.seq_q, kBM);
