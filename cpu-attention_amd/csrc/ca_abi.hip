@@ -105,8 +105,15 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t words = a->head_dim * esize(a->dtype) / 4;
 
-  // The new token first (the reference stores, then attends: paged_attn.mojo:852-863).
-  if (a->k_new) {
+  // The reference stores the new token, then attends (paged_attn.mojo:852-863).
+  // For a small batch, one token appended at lens (the serving step) is folded
+  // into the decode kernel: the wave whose tile holds position lens[s] writes it
+  // to the cache and attends it, so one launch does both.  Larger batches,
+  // several tokens, or a store at given slots (which need not be the position
+  // the row attends) go through the store kernel first.
+  const bool fused = a->k_new && !a->slots && per_seq == 1 &&
+                     a->num_seqs * a->num_heads <= kFusedAppendMaxRows;
+  if (a->k_new && !fused) {
     StoreParams sp{};
     sp.key = static_cast<const uint32_t*>(a->k_new);
     sp.value = static_cast<const uint32_t*>(a->v_new);
@@ -148,6 +155,13 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
   p.part_acc = static_cast<float*>(a->workspace);
   p.part_ml = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + acc_bytes);
   p.out = a->out;
+  if (fused) {
+    p.k_new = static_cast<const uint32_t*>(a->k_new);
+    p.v_new = static_cast<const uint32_t*>(a->v_new);
+    p.kv_stride_w = a->kv_stride * esize(a->dtype) / 4;
+    p.kc_store = static_cast<uint32_t*>(a->k_cache);
+    p.vc_store = static_cast<uint32_t*>(a->v_cache);
+  }
   return decode_launch(p, (int)a->head_dim, a->dtype == CA_BF16, st);
 }
 

@@ -128,10 +128,12 @@ struct RowState {
 };
 
 // Keys [t0, t0 + ntok) of row (seq, h): 0 < ntok <= 256, t0 % 16 == 0, t0 + ntok <= len.
-// Folds them into st.  p_lds is this wave's 256-float scratch.
-template <int E, bool BF>
+// Folds them into st.  p_lds is this wave's 256-float scratch.  newj >= 0 (wave-
+// uniform) names the key of the tile that is the token appended by this call: the
+// wave copies it from p.k_new / p.v_new into the cache before reading the tile.
+template <int E, bool BF, bool APPEND>
 __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, int64_t h,
-                                            int64_t t0, int ntok, float* p_lds,
+                                            int64_t t0, int ntok, int newj, float* p_lds,
                                             RowState<E, BF>& st) {
   using D = DecodeShape<E, BF>;
   constexpr int W = D::W, DPL = D::DPL, LPR = D::LPR, G = D::G, ES = D::ES, UNROLL = D::UNROLL;
@@ -150,6 +152,33 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
       kb = base * W + off;
       vb = (base + off) * E;
     }
+  }
+
+  // ---- the token appended by this call, at tile key newj.  Its words are read
+  // here (beside the page-table reads above, so the latencies overlap).  Right
+  // after the Q.K loop it goes to the cache: its K words land in lines the loop
+  // has just brought into L2 (4-byte writes into lines that are not resident
+  // would each cost the DRAM a read-modify-write), and its V row ahead of the
+  // P.V loads that read it back (a workgroup-scope release and acquire orders the
+  // two for the wave's lanes; on gfx950 the CU keeps them in order and the fence
+  // costs nothing).  Its logit, computed from the registers, replaces what the
+  // lane owning the key read from the slot.
+  // Nothing is stored or substituted when the key's page names no block.
+  constexpr int KNW = (W + kWave - 1) / kWave;  // K words of the new key per lane
+  uint32_t knw[KNW], qnw[KNW];
+  u32x4 vrow;
+  int64_t kbn = -1;
+  if (APPEND && newj >= 0) {
+    const uint32_t* knew = p.k_new + seq * p.kv_stride_w + h * W;
+    const uint32_t* vnew = p.v_new + seq * p.kv_stride_w + h * W;
+    const uint32_t* qwd = reinterpret_cast<const uint32_t*>(p.q) + (seq * p.q_stride + h * E) * ES / 4;
+#pragma unroll
+    for (int i = 0; i < KNW; ++i) {
+      const int w = lane + kWave * i;
+      knw[i] = w < W ? knew[w] : 0u;
+      qnw[i] = w < W ? qwd[w] : 0u;
+    }
+    vrow = lane < W / 4 ? *reinterpret_cast<const u32x4*>(vnew + 4 * lane) : u32x4{0u, 0u, 0u, 0u};
   }
 
   // ---- Q.K: keys 4*lane .. 4*lane+3 of the tile.
@@ -211,6 +240,38 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
     s[1] = (ok && key0 + 1 < ntok) ? a1 : -INFINITY;
     s[2] = (ok && key0 + 2 < ntok) ? a2 : -INFINITY;
     s[3] = (ok && key0 + 3 < ntok) ? a3 : -INFINITY;
+  }
+  if (APPEND && newj >= 0) {
+    kbn = __shfl(kb, newj >> 4);
+    const int64_t vbn = __shfl(vb, newj >> 4);
+    if (kbn >= 0) {
+      const int x = newj & (kUnit - 1);
+#pragma unroll
+      for (int i = 0; i < KNW; ++i) {
+        const int w = lane + kWave * i;
+        if (w < W) p.kc_store[kbn + (int64_t)w * p.page + x] = knw[i];
+      }
+      if (lane < W / 4)
+        *reinterpret_cast<u32x4*>(p.vc_store + (vbn + (int64_t)x * E) * ES / 4 + 4 * lane) = vrow;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < KNW; ++i) {
+      if constexpr (BF)
+        part = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(knw[i]), as_bf16x2(qnw[i]), part, false);
+      else
+        part = fmaf(__uint_as_float(knw[i]), __uint_as_float(qnw[i]), part);
+    }
+    const float logit = wave_sum(part);
+    if (kbn >= 0 && lane == (newj >> 2)) {
+      const int j = newj & 3;
+      s[0] = j == 0 ? logit : s[0];
+      s[1] = j == 1 ? logit : s[1];
+      s[2] = j == 2 ? logit : s[2];
+      s[3] = j == 3 ? logit : s[3];
+    }
   }
 
   // ---- online softmax: tile max in scaled log2 units, alpha = 2^(m_old - m_new)
@@ -333,7 +394,8 @@ __device__ __forceinline__ float merge_states(int n, Get&& get, float& mx, float
 }
 
 // One wave per 256-key tile of each row, 8 tiles per block merged in LDS.
-template <int E, bool BF>
+// APPEND: the call's one-token append is done here (p.k_new).
+template <int E, bool BF, bool APPEND>
 __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(4)))
 void decode_tiles_kernel(DecodeParams p) {
   __shared__ __attribute__((aligned(16))) float p_lds[kDecWaves][kTile];
@@ -350,7 +412,14 @@ void decode_tiles_kernel(DecodeParams p) {
   if (t0 >= len && tile != 0) return;
   RowState<E, BF> st;
   st.init();
-  if (t0 < len) decode_tile<E, BF>(p, s, h, t0, (int)min<int64_t>(kTile, len - t0), p_lds[wv], st);
+  // The appended token (lens[s] is the length before it) sits in this wave's
+  // tile when its position is one the row attends.
+  int newj = -1;
+  if (APPEND) {
+    const int64_t pos = p.lens[s];
+    if (pos >= t0 && pos < t0 + kTile && pos < len) newj = (int)(pos - t0);
+  }
+  if (t0 < len) decode_tile<E, BF, APPEND>(p, s, h, t0, (int)min<int64_t>(kTile, len - t0), newj, p_lds[wv], st);
   wave_partial<E, BF>(st, part[wv]);
   __syncthreads();
   if (wv != 0) return;
@@ -408,8 +477,12 @@ static int decode_launch_t(const DecodeParams& p, hipStream_t stream) {
   const int64_t rows = p.nseqs * p.heads;
   const int64_t gy = cdiv(p.tiles, kDecWaves);
   if (rows > 0x7fffffff || gy > 65535 || decode_workspace_slots(rows, p.tiles) > p.slots) return CA_DECLINED;
-  hipLaunchKernelGGL((decode_tiles_kernel<E, BF>), dim3((unsigned)rows, (unsigned)gy), dim3(64 * kDecWaves), 0,
-                     stream, p);
+  if (p.k_new)
+    hipLaunchKernelGGL((decode_tiles_kernel<E, BF, true>), dim3((unsigned)rows, (unsigned)gy), dim3(64 * kDecWaves),
+                       0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_tiles_kernel<E, BF, false>), dim3((unsigned)rows, (unsigned)gy), dim3(64 * kDecWaves),
+                       0, stream, p);
   int st = ca_launch_status();
   if (st != CA_OK || gy == 1) return st;
   hipLaunchKernelGGL((decode_tiles_combine_kernel<E, BF>), dim3((unsigned)cdiv(rows, 4)), dim3(256),

@@ -50,6 +50,34 @@ def test_append_one_token(cuda, dtype):
     assert_close(again, ref, dtype, paged=True)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("nseqs", [128, 129])
+def test_append_either_side_of_the_fused_limit(cuda, dtype, nseqs):
+    """A one-token append over 128 x 8 = 1024 rows is done inside the decode
+    kernel, over 129 x 8 = 1032 rows by the store kernel first: both write the
+    bytes the layout oracle says (the unwritten slots keep their NaN poison) and
+    attend the new token."""
+    h, d, page = 8, 64, 16
+    rng = random.Random(nseqs)
+    lens = [rng.randrange(0, 300) for _ in range(nseqs)]
+    lens[:3] = [0, 15, 16]  # empty, last slot of a page, first slot of a new page
+    # Stage one token more than lens, so that position lens[s] lies in a page of
+    # sequence s (the helper points every row's page-table padding at one shared
+    # block); the append overwrites that token.
+    q, kc, vc, bt, ks, vs = stage([n + 1 for n in lens], h, d, page, dtype, seed=nseqs, device=cuda)
+    ks, vs = [k[:, :n] for k, n in zip(ks, lens)], [v[:, :n] for v, n in zip(vs, lens)]
+    kw, vw = cache_words(kc), cache_words(vc)
+    g = torch.Generator().manual_seed(7)
+    kn, vn = (torch.randn(nseqs, 1, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    out = flash_attn_with_kvcache(q, kc, vc, k=kn, v=vn, cache_seqlens=seqlens, page_table=bt)
+    assert_close(out, reference(q, *appended(ks, vs, kn, vn), d ** -0.5), dtype, paged=True)
+    layout.store(kw, vw, row_words(kn[:, 0]), row_words(vn[:, 0]),
+                 layout.append_slots(lens, bt.cpu().numpy(), page), page)
+    np.testing.assert_array_equal(cache_words(kc), kw)
+    np.testing.assert_array_equal(cache_words(vc), vw)
+
+
 @pytest.mark.parametrize("host_checks", [True, False])
 def test_uneven_lengths(cuda, host_checks):
     """Lopsided batches (the reference sweeps thread counts here; the GPU splits every
