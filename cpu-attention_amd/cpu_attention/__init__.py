@@ -1,13 +1,15 @@
-"""cpu-attention's three attention ops on AMD Instinct MI355X (gfx950), with
-flash-attn's API.
+# Derived from ducviet00/cpu-attention (cpu_attention/__init__.py), Apache
+# License 2.0; modified for the MI355X build (see NOTICE at the repository root).
+# The export list is the original package's, so that imports keep working.
 
-A drop-in for ducviet00/cpu-attention's package: the same functions, arguments,
-errors and cache layout, computed by hand-written CDNA4 HIP kernels behind a C ABI
-(``libcpu_attention_hip.so``).  The paged decode path mirrors
-``flash_attn_with_kvcache``; the cache layout is head-major
-``[num_blocks, nheads_k, page_block_size, headdim]`` rather than flash-attn's
-page-major one, because K is stored transposed inside the page, so
-``reshape_and_cache`` (vLLM's signature) is exported to write it.
+"""The three attention ops of ducviet00/cpu-attention, computed on an AMD Instinct
+MI355X (gfx950) by hand-written CDNA4 kernels behind a C ABI
+(``libcpu_attention_hip.so``), with the original package's flash-attn-style
+functions, arguments, errors and cache layout.
+
+The KV cache is head-major, ``[num_blocks, nheads_k, page_block_size, headdim]``
+with K transposed inside each page -- not flash-attn's page-major layout -- so
+``reshape_and_cache`` (vLLM's signature) is exported to fill it.
 """
 
 from .cache import reshape_and_cache

@@ -1,3 +1,10 @@
+# The module surface here (module(), runtime(), workspace(), physical_cores(),
+# llc_bytes(), DTYPES, HEAD_DIMS, and the decode/store/flash entries with their
+# positional arguments and None/int returns) follows ducviet00/cpu-attention's
+# cpu_attention/_kernel.py and native module, Apache License 2.0, so that engine
+# code written against it runs unchanged (see NOTICE at the repository root); the
+# implementation is this build's own.
+
 """Loads the gfx950 kernel library and exposes the reference's native entries.
 
 The reference loads a Mojo CPython extension per CPU tier (cpu_attention/_kernel.py:52-84
@@ -23,6 +30,7 @@ Environment: ``CPU_ATTENTION_LIB`` names another build of the library.
 """
 
 import ctypes
+import functools
 import os
 import threading
 
@@ -449,37 +457,48 @@ def runtime():
     return ABI_VERSION
 
 
-def _cached(fn):
-    value = []
-    return lambda: value[0] if value else value.append(fn()) or value[0]
-
-
-@_cached
+@functools.lru_cache(maxsize=None)
 def physical_cores():
-    """Physical cores visible to this process, from the sysfs topology."""
-    cores = set()
+    """Physical cores this process may run on: the CPUs of its affinity mask,
+    counted once per set of hardware threads that share a core (the sysfs
+    ``thread_siblings_list`` of each CPU).  Falls back to the CPU count."""
     try:
-        for cpu in range(os.cpu_count() or 1):
-            base = f"/sys/devices/system/cpu/cpu{cpu}/topology"
-            with open(f"{base}/core_id") as f, open(f"{base}/physical_package_id") as g:
-                cores.add((g.read().strip(), f.read().strip()))
-    except OSError:
-        cores = set()
-    return len(cores) or (os.cpu_count() or 1)
-
-
-@_cached
-def llc_bytes():
-    """Last-level cache size of the host, from sysfs (32 MiB if unknown)."""
-    for idx in (3, 2, 1, 0):
+        cpus = sorted(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        cpus = list(range(os.cpu_count() or 1))
+    cores = set()
+    for cpu in cpus:
         try:
-            with open(f"/sys/devices/system/cpu/cpu0/cache/index{idx}/size") as f:
-                text = f.read().strip()
+            with open(f"/sys/devices/system/cpu/cpu{cpu}/topology/thread_siblings_list") as f:
+                cores.add(f.read().strip())
         except OSError:
+            return len(cpus) or 1
+    return len(cores) or len(cpus) or 1
+
+
+@functools.lru_cache(maxsize=None)
+def llc_bytes():
+    """Size in bytes of the largest-level cache sysfs lists for CPU 0 (the last
+    level), or 32 MiB when sysfs says nothing."""
+    base = "/sys/devices/system/cpu/cpu0/cache"
+    best = (0, 0)  # (level, bytes)
+    try:
+        names = [n for n in os.listdir(base) if n.startswith("index")]
+    except OSError:
+        names = []
+    for name in names:
+        try:
+            with open(f"{base}/{name}/level") as f:
+                level = int(f.read())
+            with open(f"{base}/{name}/size") as f:
+                text = f.read().strip().upper()
+        except (OSError, ValueError):
             continue
-        unit = {"K": 1 << 10, "M": 1 << 20}.get(text[-1], 1)
-        return int(text.rstrip("KM")) * unit
-    return 32 << 20
+        scale = {"K": 1 << 10, "M": 1 << 20, "G": 1 << 30}.get(text[-1:], 1)
+        digits = text.rstrip("KMG")
+        if digits.isdigit():
+            best = max(best, (level, int(digits) * scale))
+    return best[1] or 32 << 20
 
 
 _WS = {}
