@@ -26,6 +26,13 @@ Method (the reference's benchmarks/bench.py, moved to a GPU):
   synchronisation per decode or store call.  ``off`` is the serving setting
   (``CPU_ATTENTION_HOST_CHECKS=0``); the kernels stay in bounds either way.
 * Paged rows run at page sizes 16 and 32 and keep the best, as the reference does.
+* ``--counters`` adds rocprofv3 columns to every row: the row's own arm runs
+  again, five calls without flushes, in a child process under ``rocprofv3``
+  (``counters.py``): a kernel trace (device time of the library's kernels per
+  call), ``FETCH_SIZE`` and ``WRITE_SIZE`` (HBM bytes per call, each scaled by
+  what the counter reads for a 256 MiB copy in the same process), and for
+  prefill rows ``MfmaUtil`` (MFMA-busy cycles over elapsed cycles).  The last
+  call of each pass is the one reported.
 * Rooflines: HBM 8 TB/s, dense MFMA 2.5 PFLOP/s bf16 and 157.3 TFLOP/s fp32.
   Decode bytes are the algorithmic ones (K and V of every visible token once, q,
   out, the new token's K/V read and written, page-table entries and lengths);
@@ -98,9 +105,37 @@ class Flusher:
         self.buf.add_(1)
 
 
-def measure(fns, flush):
+PROFILE = {}  # --profile-row: the row and arm whose calls a rocprofv3 child records
+
+
+class Profiled(Exception):
+    """Raised once the profiled row's calls are done (nothing else runs)."""
+
+
+def profile_calls(fn, calls=5):
+    """The counters' calibration copy (256 MiB), then `calls` calls of `fn`."""
+    src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    for _ in range(calls):
+        fn()
+    torch.cuda.synchronize()
+
+
+def measure(fns, flush, row=None):
     """3 warmup + 10 timed calls per arm, rotated, caches flushed before each call.
-    Returns per arm: API wall clock and device time (µs): median, min, max."""
+    Returns per arm: API wall clock and device time (µs): median, min, max.
+    In --profile-row mode, runs the chosen row's arm for rocprofv3 instead (and
+    returns None for every other row); `row` is (name, dtype)."""
+    if PROFILE:
+        if row is not None and row != (PROFILE["row"], PROFILE["dtype"]):
+            return None
+        arm = PROFILE["arm"] if PROFILE["arm"] in fns else sorted(fns)[0]
+        profile_calls(fns[arm])
+        raise Profiled()
     names = list(fns)
     for n in names:
         for _ in range(WARMUP):
@@ -231,12 +266,14 @@ def reference_rows(args, dev, flush, emit):
                 name = label(kind, spec)
                 if args.only not in name or args.dtype not in ("both", dt):
                     continue
+                if PROFILE and (name, dt) != (PROFILE["row"], PROFILE["dtype"]):
+                    continue
                 torch.manual_seed(0)
                 if kind == "flash":
                     fns, out, ref, work = flash_row(spec, DT[dt], dev)
                 else:
                     fns, out, ref, work = paged_row(spec, DT[dt], dev)
-                timing = measure(fns, flush)
+                timing = measure(fns, flush, (name, dt))
                 ours = best(timing, "ours")
                 base = ref if ref in timing else None
                 emit(kind, name, dt, spec, timing, ours, base, out, work)
@@ -255,15 +292,18 @@ def baseline_rows(args, dev, flush, emit):
         if args.only not in name:
             continue
         fns, out, ref, work = flash_row(spec, DT[dt], dev, qkv_fused="fused" in name)
-        timing = measure(fns, flush)
-        emit(kind, name, dt, spec, timing, "ours", ref if ref in timing else None, out, work)
+        timing = measure(fns, flush, (name, dt))
+        if timing is not None:
+            emit(kind, name, dt, spec, timing, "ours", ref if ref in timing else None, out, work)
     # cfg2: decode fp32 N=8 H=16 E=64 P=16, lens U[17,2047], append one token
     if args.dtype in ("both", "fp32") and args.only in "cfg2 decode":
         lens = [int(x) for x in rng.integers(17, 2048, size=8)]
         spec = (8, lens, 16, 64, True)
         fns, out, _, work = paged_row(spec, torch.float32, dev)
         fns = {k: f for k, f in fns.items() if k.endswith("p16")}
-        emit("paged", "cfg2 decode", "fp32", spec, measure(fns, flush), "ours p16", None, out, work)
+        timing = measure(fns, flush, ("cfg2 decode", "fp32"))
+        if timing is not None:
+            emit("paged", "cfg2 decode", "fp32", spec, timing, "ours p16", None, out, work)
     # cfg3: decode bf16 N=64 H=32 E=128 P=32, lens U[17,2047], random-permutation table, no append
     if args.dtype in ("both", "bf16") and args.only in "cfg3 decode":
         n, h, e, page = 64, 32, 128, 32
@@ -279,8 +319,10 @@ def baseline_rows(args, dev, flush, emit):
         fns = {"ours p32": lambda: out.__setitem__("ours p32", cpu_attention.flash_attn_with_kvcache(
             q, kc, vc, cache_seqlens=sl, page_table=table))}
         work = decode_bytes([int(x) for x in lens], h, e, 2, False, sum(-(-int(x) // page) for x in lens))
-        emit("paged", "cfg3 decode", "bf16", (n, [int(x) for x in lens], h, e, False), measure(fns, flush),
-             "ours p32", None, out, work)
+        timing = measure(fns, flush, ("cfg3 decode", "bf16"))
+        if timing is not None:
+            emit("paged", "cfg3 decode", "bf16", (n, [int(x) for x in lens], h, e, False), timing,
+                 "ours p32", None, out, work)
         del kc, vc
     # cfg5: store 128 prompts (U[64,1024], 10% padding slots) then decode steps with append
     if args.dtype in ("both", "bf16") and args.only in "cfg5 store + decode":
@@ -309,7 +351,9 @@ def baseline_rows(args, dev, flush, emit):
         fns = {"ours": lambda: cpu_attention.reshape_and_cache(key, val, kc, vc, sm)}
         stored = int(keep.sum())
         work = 2 * 2 * stored * h * e * 2 + len(slot_map) * 8
-        emit("store", "cfg5 store", "bf16", (n, total, h, e, page), measure(fns, flush), "ours", None, {}, work)
+        timing = measure(fns, flush, ("cfg5 store", "bf16"))
+        if timing is not None:
+            emit("store", "cfg5 store", "bf16", (n, total, h, e, page), timing, "ours", None, {}, work)
         sl = torch.tensor(lens, dtype=torch.int32, device=dev)
         q = torch.randn(n, 1, h, e, generator=g, device=dev).to(torch.bfloat16)
         kn, vn = (torch.randn(n, 1, h, e, generator=g, device=dev).to(torch.bfloat16) for _ in range(2))
@@ -322,8 +366,15 @@ def baseline_rows(args, dev, flush, emit):
             step[0] = (step[0] + 1) % steps
         work = decode_bytes([int(m) + steps // 2 for m in lens], h, e, 2, True,
                             sum(-(-(int(m) + steps // 2) // page) for m in lens))
-        emit("paged", "cfg5 decode step", "bf16", (n, [int(x) for x in lens], h, e, True),
-             measure({"ours": decode_step}, flush), "ours", None, out, work)
+        timing = measure({"ours": decode_step}, flush, ("cfg5 decode step", "bf16"))
+        if timing is not None:
+            emit("paged", "cfg5 decode step", "bf16", (n, [int(x) for x in lens], h, e, True), timing,
+                 "ours", None, out, work)
+
+
+def row_work(kind, work):
+    """A row's algorithmic bytes (prefill: q, k, v and out once)."""
+    return work[1] if kind == "flash" else work
 
 
 def main():
@@ -334,11 +385,29 @@ def main():
     ap.add_argument("--dtype", choices=("bf16", "fp32", "both"), default="both")
     ap.add_argument("--host-checks", choices=("on", "off"), default="on")
     ap.add_argument("--git", default="", help="commit label for the report (default: git rev-parse)")
+    ap.add_argument("--counters", action="store_true",
+                    help="add rocprofv3 columns (kernel time, HBM bytes, MFMA busy) to every row")
+    ap.add_argument("--profile-row", nargs=3, metavar=("NAME", "DTYPE", "ARM"),
+                    help="(used by --counters) run only this row's arm, for a rocprofv3 child")
     args = ap.parse_args()
     _kernel.set_host_checks(args.host_checks == "on")
     if not torch.cuda.is_available():
         print("bench: no GPU visible", file=sys.stderr)
         return 1
+    if args.profile_row:
+        PROFILE.update(row=args.profile_row[0], dtype=args.profile_row[1], arm=args.profile_row[2])
+        # build only the profiled row (cfg5's two rows share one setup)
+        args.only = "cfg5" if args.profile_row[0].startswith("cfg5") else args.profile_row[0]
+        try:
+            if args.table in ("reference", "both"):
+                reference_rows(args, torch.device("cuda:0"), lambda: None, None)
+            if args.table in ("baseline", "both"):
+                baseline_rows(args, torch.device("cuda:0"), lambda: None, None)
+        except Profiled:
+            print("profiled", flush=True)
+            return 0
+        print(f"bench: no row {args.profile_row[0]!r} ({args.profile_row[1]})", file=sys.stderr)
+        return 2
     dev = torch.device("cuda:0")
     flush = Flusher(dev)
     env = dict(machine=platform.node(), gpu=torch.cuda.get_device_name(0), host_checks=args.host_checks,
@@ -368,6 +437,18 @@ def main():
             row["max_diff"] = (out[ours].float() - out[base].float()).abs().max().item()
             line += f"  {base} gpu {timing[base]['gpu']['median']:9.1f} us  ratio {row['ratio']:.2f}" \
                     f"  diff {row['max_diff']:.1e}"
+        if args.counters:
+            import counters
+            row["counters"] = counters.collect(
+                name, dt, ours, kind, table="baseline" if name.startswith("cfg") else "reference",
+                host_checks=args.host_checks)
+            c = row["counters"]
+            if c.get("kernel_us"):
+                line += f"  | rocprof {c['kernel_us']:.1f} us"
+            if c.get("hbm_bytes"):
+                line += f", HBM {c['hbm_bytes'] / 1e6:.1f} MB ({c['hbm_bytes'] / max(row_work(kind, work), 1):.2f}x)"
+            if c.get("mfma_util_pct") is not None:
+                line += f", MFMA busy {c['mfma_util_pct']:.1f}%"
         print(line, flush=True)
         rows.append(row)
         if args.json:

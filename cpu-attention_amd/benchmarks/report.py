@@ -4,7 +4,9 @@
 
 One table per kind (prefill, paged decode, store): per row the device-time
 median (min-max) in µs, the API wall clock, the achieved rate against the
-MI355X roofline, and for prefill the ratio to torch SDPA's fused kernels.
+MI355X roofline, for prefill the ratio to torch SDPA's fused kernels, and with
+``bench.py --counters`` the rocprofv3 columns (kernel time, HBM bytes against the
+algorithmic ones, MFMA busy for prefill).
 """
 
 import argparse
@@ -43,8 +45,12 @@ def tables(run):
             continue
         rate = "TFLOP/s (of MFMA peak) | GB/s" if kind == "flash" else "GB/s (of 8 TB/s)"
         extra = " | SDPA gpu µs | ours / SDPA" if kind == "flash" else ""
+        counted = any("counters" in x for x in rows)
+        if counted:
+            extra += " | rocprof kernel µs | HBM MB (x algorithmic)" + (" | MFMA busy" if kind == "flash" else "")
+        ncols = (4 if kind == "flash" else 1) + ((3 if kind == "flash" else 2) if counted else 0)
         out += [f"**{title}**\n", f"| row | dtype | gpu µs, median (min-max) | API µs | {rate}{extra} |",
-                "|---|---|---:|---:|---:|" + ("---:|---:|---:|" if kind == "flash" else "")]
+                "|---|---|---:|---:|" + "---:|" * ncols]
         for x in rows:
             t = x["timing"][x["ours"]]
             name = x["name"] if x["name"].startswith("cfg") else label(x["kind"], x["shape"])
@@ -60,6 +66,16 @@ def tables(run):
                     line += f" | {us(x['timing'][x['ref']]['gpu']['median'])} | **{x['ratio']:.2f}**"
                 else:
                     line += " | - | -"
+            if counted:
+                c = x.get("counters", {})
+                work = x["gbs"] * t["gpu"]["median"] * 1e-6 * 1e9 if "gbs" in x else None
+                line += f" | {c['kernel_us']:.1f}" if "kernel_us" in c else " | -"
+                if "hbm_bytes" in c:
+                    line += f" | {c['hbm_bytes'] / 1e6:,.1f}" + (f" ({c['hbm_bytes'] / work:.2f}x)" if work else "")
+                else:
+                    line += " | -"
+                if kind == "flash":
+                    line += f" | {c['mfma_util_pct']:.1f}%" if "mfma_util_pct" in c else " | -"
             out.append(line + " |")
         out.append("")
     return "\n".join(out)

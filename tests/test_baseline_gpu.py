@@ -39,7 +39,7 @@ def dense_kv(kc, vc, table_row, length, page):
 
 def test_cfg3_decode_bf16_full_size(cuda):
     """N=64 H=32 E=128 page=32, lens U[17,2047], random-permutation page table, no
-    append; the oracle checks 8 sampled sequences (all heads)."""
+    append; the oracle checks every sequence (all heads)."""
     n, h, e, page = 64, 32, 128, 32
     rng = np.random.default_rng(3)
     lens = rng.integers(17, 2048, size=n)
@@ -49,7 +49,7 @@ def test_cfg3_decode_bf16_full_size(cuda):
     out = flash_attn_with_kvcache(q, kc, vc, cache_seqlens=seqlens, page_table=table)
     assert torch.isfinite(out).all()
     tcpu = table.cpu()
-    for s in (0, 1, int(np.argmax(lens)), int(np.argmin(lens)), 20, 33, 47, 63):
+    for s in range(n):
         k, v = dense_kv(kc, vc, tcpu[s], int(lens[s]), page)
         ref = attention(values(q[s:s + 1]), k[None], v[None], e ** -0.5)
         assert_close(out[s:s + 1], ref, torch.bfloat16, paged=True)
