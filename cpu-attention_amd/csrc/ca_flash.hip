@@ -14,8 +14,8 @@
 //   S^T = K Q^T   32x32x16 MFMAs with keys as rows and queries as columns, so a
 //                 lane ends up owning one query and 16 keys of each 32-key half;
 //   softmax       per lane (its query) against a max fixed at the first tile;
-//                 rows whose later logits outgrow it by more than 2^20 are redone
-//                 by a safe pass with a running max;
+//                 rows whose later logits outgrow it by more than 64 in log2
+//                 units are redone by a safe pass with a running max;
 //   O^T += V^T P^T the probabilities are already in the B-operand layout of the
 //                 MFMA (no LDS round trip); P is rounded to bf16 as the reference's
 //                 bf16 policy does (flash_vec.mojo:255-259), fp32 accumulation.
@@ -543,7 +543,11 @@ struct P64Rows {
   // exceeds the fast walk's headroom (or is NaN).
   template <int PAR, bool PV, bool SN, bool SOFT, typename F>
   __device__ __forceinline__ bool step(const uint16_t* vb, const uint16_t* kb, float c, F&& loads) {
-    constexpr float kHeadSum = 1048576.f;  // a lane's p summed over a tile <= 2^20
+    // A lane's p summed over a tile <= 2^64.  p taken against a max that a later
+    // logit exceeds is still exact in floating point (no precision is lost to a
+    // large exponent); the bound only keeps the sums finite: l stays below 2^71
+    // over any 4096 keys, so O = sum p V cannot overflow fp32 unless |V| > 2^57.
+    constexpr float kHeadSum = 18446744073709551616.f;
     constexpr int NPVo = PV ? NPV : 0, NOP = NPVo + (SN ? NSK : 0), NM = 2 * NOP;
     constexpr int NSLOT = NM > 0 ? NM : 1, NSC = SOFT ? 64 : 0;
     static_assert(NSC % NSLOT == 0, "scores spread evenly over the MFMA slots");
@@ -828,8 +832,8 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
       int t = 0;
       if (nkt_w > 0) {
         // Tile 0: its S, the row max fixed at its own (never refreshed: the sum
-        // of a lane's p over a tile stays below 2^20 unless a later logit
-        // exceeds the fixed max by about 20 in log2 units, which `bad` records
+        // of a lane's p over a tile stays below 2^64 unless a later logit
+        // exceeds the fixed max by about 64 in log2 units, which `bad` records
         // for the safe pass), then the softmax of tile 0 beside the S of tile 1.
         w.template step<1, false, true, false>(Vs, kbuf(0), a.c, [] {});
         P64Rows<E>::mfma_guard();

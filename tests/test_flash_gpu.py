@@ -145,17 +145,22 @@ def test_cfg4_prefill_full_size_sampled(cuda):
 
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
-def test_logits_outgrowing_the_first_tile(cuda, d, causal):
+@pytest.mark.parametrize("gap", [40, 100])
+def test_logits_outgrowing_the_first_tile(cuda, d, causal, gap):
     """Keys far past the first 64 whose logits exceed every logit of the first key
-    tile by far more than 2^20 in probability: the bf16 kernel's fast walk keeps
-    the first tile's row max, so those rows must be recomputed with a running max
-    (some waves of a block take that path, others do not)."""
+    tile by about `gap` log2 units.  The bf16 kernel's fast walk keeps the first
+    tile's row max, so p reaches about 2^gap: up to 2^64 per tile it carries on
+    (the values are exact, only large), past that those rows are recomputed with a
+    running max (some waves of a block take that path, others do not)."""
     g = torch.Generator().manual_seed(11)
     b, sq, sk, h = 2, 300, 700, 2
     q = (torch.randn(b, sq, h, d, generator=g) + 1.0).bfloat16()
     k = torch.randn(b, sk, h, d, generator=g)
-    k[:, 200] = 6.0  # q.k ~ 6d: ~68 (d=128) above the others after scaling
-    k[:, 650] = 5.0
+    # q ~ N(1, 1): a key of constant `big` has a scaled logit near big * sqrt(d) *
+    # log2(e) in log2 units, the others stay within a few units of 0
+    big = (gap + 4) / (1.4427 * d ** 0.5)
+    k[:, 200] = big
+    k[:, 650] = big - 0.5
     k = k.bfloat16()
     v = torch.randn(b, sk, h, d, generator=g).bfloat16()
     q, k, v = q.to(cuda), k.to(cuda), v.to(cuda)
@@ -175,10 +180,13 @@ def test_safe_pass_for_one_pass_of_a_causal_pair(cuda, d, bad_pass):
     b, L, h = 1, 512, 2
     q = torch.randn(b, L, h, d, generator=g) * 0.5 + 1.0
     k = torch.randn(b, L, h, d, generator=g) * 0.5
+    # a key whose logits sit about 100 log2 units above the first tile's (past the
+    # fast walk's 2^64 headroom)
+    big = 104 / (1.4427 * d ** 0.5)
     if bad_pass == 0:
-        k[:, 400] = 6.0  # seen only by rows >= 400 (pass 0)
+        k[:, 400] = big  # seen only by rows >= 400 (pass 0)
     else:
-        k[:, 200] = 6.0  # seen by every row >= 200: rows of pass 0 get q < 0 for it
+        k[:, 200] = big  # seen by every row >= 200: rows of pass 0 get q < 0 for it
         q[:, 256:] = -q[:, 256:]
     q, k = q.bfloat16().to(cuda), k.bfloat16().to(cuda)
     v = torch.randn(b, L, h, d, generator=g).bfloat16().to(cuda)
