@@ -72,11 +72,12 @@ RAMP_S = 0.2  # seconds of back-to-back calls before each leg's warm-up
 METRIC = "decode HBM GB/s + µs/call; prefill TFLOP/s (bf16) vs MI355X roofline"
 
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of --profile-pass on
-# MI355X: the calibration copy, then the decode kernels and the prefill kernel.
+# MI355X: the calibration copy, then the fifth of five calls of the decode and the
+# prefill kernel.
 TRAFFIC = {
-    "copy": {"fetch_kib": 524307.7, "write_kib": 1048576.0},
-    "decode": {"fetch_kib": 543466.4, "write_kib": 512.0},
-    "prefill": {"fetch_kib": 312573.0, "write_kib": 152576.0},
+    "copy": {"fetch_kib": 524315.375, "write_kib": 1048576.0},
+    "decode": {"fetch_kib": 543394.5, "write_kib": 512.0},
+    "prefill": {"fetch_kib": 313687.062, "write_kib": 152576.0},
 }
 
 # The reference's published CPU figures (medians at its Python API, L2/L3 flushed,
