@@ -523,6 +523,11 @@ def clock_trace(dev, mod, rt, calls):
           f"median {np.median(us[calls // 2:]):.1f} us", flush=True)
 
 
+def progress(what, t0):
+    """One line on stderr per finished leg (stdout carries only the JSON line)."""
+    print(f"bench: {what} done ({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -557,6 +562,7 @@ def main():
         clock_trace(dev, mod, rt, args.clock_trace)
         return
 
+    t0 = time.perf_counter()
     w = decode_workload(dev)
     out = torch.empty_like(w["q"])
 
@@ -588,6 +594,7 @@ def main():
     }
     del w
     torch.cuda.empty_cache()
+    progress("decode (cfg3)", t0)
 
     if not args.no_prefill:
         N, L, H, E = 4, 4096, 32, 128
@@ -615,17 +622,21 @@ def main():
         }
         del qkv, q, k, v
         torch.cuda.empty_cache()
+        progress("prefill (cfg4)", t0)
 
     if not args.no_configs:
         res["configs"] = run_configs(dev, mod, rt)
         torch.cuda.empty_cache()
+        progress("configs", t0)
 
     if not args.no_cpu:
         w = decode_workload(dev)
         res["cpu_baseline"] = cpu_decode_baseline(w)
         del w
+        progress("CPU decode baseline", t0)
         if not args.no_prefill:
             res["prefill"]["cpu_baseline"] = cpu_prefill_baseline()
+            progress("CPU prefill baseline", t0)
     print(json.dumps(res), flush=True)
 
 

@@ -51,16 +51,19 @@ def test_append_one_token(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("nseqs", [128, 129])
-def test_append_either_side_of_the_fused_limit(cuda, dtype, nseqs):
-    """A one-token append over 128 x 8 = 1024 rows is done inside the decode
-    kernel, over 129 x 8 = 1032 rows by the store kernel first: both write the
-    bytes the layout oracle says (the unwritten slots keep their NaN poison) and
-    attend the new token."""
+@pytest.mark.parametrize("nseqs", [2, 129, 600])
+def test_append_in_the_decode_kernel(cuda, dtype, nseqs):
+    """One token appended per sequence is written and attended by the decode kernel
+    itself (one launch), from 16 rows to 4800: the cache holds the bytes the layout
+    oracle says (the unwritten slots keep their NaN poison) and the output attends
+    the new token.  Edge positions: an empty row, the last slot of a page, the first
+    slot of a new page, and a row past one block's 2048 keys, whose blocks meet in
+    the combine kernel."""
     h, d, page = 8, 64, 16
     rng = random.Random(nseqs)
     lens = [rng.randrange(0, 300) for _ in range(nseqs)]
-    lens[:3] = [0, 15, 16]  # empty, last slot of a page, first slot of a new page
+    edge = [0, 15, 16, 2100][:nseqs]
+    lens[:len(edge)] = edge
     # Stage one token more than lens, so that position lens[s] lies in a page of
     # sequence s (the helper points every row's page-table padding at one shared
     # block); the append overwrites that token.
