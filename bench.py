@@ -3,7 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
                     [--no-configs] [--profile-pass] [--clock-trace N]
 
-The headline step is one call of the paged decode over BASELINE config 3 (bf16,
+The headline step is one call of the paged decode over BASELINE cfg3 (bf16,
 N=64 H=32 E=128 page 32, cache_seqlens U[17,2047], random-permutation page table,
 no append): the north-star decode workload, HBM-bound.  ``value`` is the
 whole-job throughput in algorithmic HBM bytes per second over the K timed steps
@@ -23,7 +23,7 @@ The JSON line also carries:
 
 * ``roofline`` for the decode kernel: algorithmic bytes per call / the event-timed
   average call duration against MI355X's 8 TB/s;
-* ``prefill``: BASELINE config 4 (bf16 causal N=4 L=S=4096 H=32 E=128, q/k/v
+* ``prefill``: BASELINE cfg4 (bf16 causal N=4 L=S=4096 H=32 E=128, q/k/v
   strided chunks of a fused projection) in TFLOP/s against the 2.5 PFLOP/s dense
   bf16 MFMA peak, with its own roofline object;
 * ``configs``: every other BASELINE config -- cfg1 (prefill N=1 L=S=128), cfg2
@@ -34,8 +34,9 @@ The JSON line also carries:
   256 MB MALL holds the inputs: the reference's method, benchmarks/bench.py:112-127),
   and the host wall time per call at the Python API;
 * ``cpu_baseline``: the oracle's C port of the reference's CPU decode (the Mojo
-  reference cannot be built here) on the box's host cores, on a bounded sample of
-  the same workload, labelled as a substitute, with the reference's own published
+  reference cannot be built here) on the box's physical host cores, over the whole
+  cfg3 batch for CPU_BUDGET_S seconds (and the prefill port on one (batch, head) of
+  cfg4 for as long), labelled as a substitute, with the reference's own published
   CPU figures beside it.
 
 ``roofline.traffic`` is the HBM bytes one call moves, from rocprofv3 --pmc runs of
@@ -69,6 +70,7 @@ BF16_PEAK_TFLOPS = 2500.0
 COPY_BYTES = 1 << 30  # the calibration copy of --profile-pass
 FLUSH_BYTES = 1 << 30  # written between cold samples: > 2 x (256 MB MALL + L2)
 RAMP_S = 0.2  # seconds of back-to-back calls before each leg's warm-up
+CPU_BUDGET_S = 8.0  # seconds of back-to-back calls per CPU baseline
 METRIC = "decode HBM GB/s + µs/call; prefill TFLOP/s (bf16) vs MI355X roofline"
 
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of --profile-pass on
@@ -403,13 +405,13 @@ def run_configs(dev, mod, rt):
 # ---------------------------------------------------------------------------
 # CPU baseline (the oracle's C port: test infrastructure, timed here only)
 # ---------------------------------------------------------------------------
-def cpu_decode_baseline(w, budget_s=4.0):
-    """The C port of the reference's CPU decode on the host's physical cores, on the
-    first sequences of the same batch (about 1/8 of its K/V)."""
+def cpu_decode_baseline(w, budget_s=CPU_BUDGET_S):
+    """The C port of the reference's CPU decode on the host's physical cores, over the
+    whole cfg3 batch, called back to back for ``budget_s`` seconds."""
     from cpu_attention import _kernel as K
     from oracle import cport
 
-    ns = 8
+    ns = w["n"]
     page, h, e = w["page"], w["h"], w["e"]
     lens = w["lens"][:ns]
     pages = [-(-int(m) // page) for m in lens]
@@ -428,7 +430,7 @@ def cpu_decode_baseline(w, budget_s=4.0):
     while True:
         cport.decode(q, kc, vc, lens, table, page, e ** -0.5, True, threads)
         reps += 1
-        if time.perf_counter() - t0 >= budget_s or reps >= 50:
+        if time.perf_counter() - t0 >= budget_s and reps >= 3:
             break
     dt = (time.perf_counter() - t0) / reps
     nbytes = sum(2 * int(m) * h * e * 2 for m in lens) + 2 * ns * h * e * 2
@@ -438,12 +440,14 @@ def cpu_decode_baseline(w, budget_s=4.0):
                     "the oracle's C/OpenMP port of its decode algorithm, a substitute, with the reference's "
                     "published CPU figures beside it",
             "sample": f"C port (oracle/ca_oracle.c, OpenMP) of the reference's paged decode on the "
-                      f"first {ns} of the 64 sequences ({nbytes / 1e6:.0f} MB of K/V, bf16), "
-                      f"{reps} calls, {dt * 1e3:.2f} ms/call",
+                      f"whole cfg3 batch ({ns} sequences, {nbytes / 1e6:.0f} MB of K/V, bf16), "
+                      f"{reps} calls in {reps * dt:.1f} s, {dt * 1e3:.2f} ms/call",
             "published": PUBLISHED["decode"]}
 
 
-def cpu_prefill_baseline(budget_s=4.0):
+def cpu_prefill_baseline(budget_s=CPU_BUDGET_S):
+    """The C port of the reference's prefill on the host's physical cores, one
+    (batch, head) of cfg4 per call, called back to back for ``budget_s`` seconds."""
     from cpu_attention import _kernel as K
     from oracle import bf16, cport
 
@@ -455,7 +459,7 @@ def cpu_prefill_baseline(budget_s=4.0):
     while True:
         cport.flash(q, k, v, e ** -0.5, True, True, threads)
         reps += 1
-        if time.perf_counter() - t0 >= budget_s or reps >= 20:
+        if time.perf_counter() - t0 >= budget_s and reps >= 3:
             break
     dt = (time.perf_counter() - t0) / reps
     flop = 4 * b * h * e * L * (L + 1) / 2
@@ -466,7 +470,7 @@ def cpu_prefill_baseline(budget_s=4.0):
                     f"here); it runs about {pub / max(rate, 1e-9):.0f}x below the reference's published "
                     "rate, so read the published figure as the CPU baseline",
             "sample": f"C port of the reference's prefill, one (batch, head) of the config "
-                      f"(L=S=4096 E=128 causal bf16), {reps} calls, {dt * 1e3:.1f} ms/call",
+                      f"(L=S=4096 E=128 causal bf16), {reps} calls in {reps * dt:.1f} s, {dt * 1e3:.1f} ms/call",
             "published": PUBLISHED["prefill"]}
 
 

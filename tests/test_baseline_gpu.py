@@ -1,7 +1,7 @@
-"""The BASELINE decode workloads at full size on the GPU (size-independent checks
-plus the float64 oracle on sampled sequences), and the config-4 store + decode
-loop with the cache bytes compared to the layout oracle after staging and after
-every step."""
+"""The BASELINE decode workloads at full size on the GPU: cfg3 with every sequence
+checked against the float64 oracle, cfg2 with every row, and cfg5's store + decode
+loop with the cache bytes compared to the layout oracle after staging and after the
+first and last steps."""
 
 import numpy as np
 import pytest

@@ -107,17 +107,17 @@ def test_north_star_tolerance_fp32(cuda, causal):
 
 
 def test_cfg1_prefill_bf16(cuda):
-    """N=1 L=S=128 H=16 E=64 causal bottom-right, bf16."""
+    """BASELINE cfg1: N=1 L=S=128 H=16 E=64 causal bottom-right, bf16."""
     run(1, 128, 128, 16, 64, torch.bfloat16, True, seed=0, device=cuda)
 
 
 def test_cfg4_cross_shape(cuda):
-    """BASELINE config 3 (cross shape): N=8 L=1 S=2048 E=32 H=32, non-causal, bf16."""
+    """BASELINE cfg4 (its cross shape): N=8 L=1 S=2048 E=32 H=32, non-causal, bf16."""
     run(8, 1, 2048, 32, 32, torch.bfloat16, False, seed=8, device=cuda)
 
 
 def test_cfg4_prefill_full_size_sampled(cuda):
-    """N=4 L=S=4096 H=32 E=128 causal bf16, q/k/v strided chunks of a
+    """BASELINE cfg4: N=4 L=S=4096 H=32 E=128 causal bf16, q/k/v strided chunks of a
     fused [N*L, 3*H*E] projection.  The whole output is computed; the float64 oracle
     checks sampled (batch, head) pairs on sampled rows (first, last, tile edges,
     random)."""

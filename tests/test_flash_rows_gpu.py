@@ -71,7 +71,7 @@ def test_scale_and_large_logits(cuda):
 
 
 def test_cfg4_cross_shape_rows(cuda):
-    """BASELINE config 3's cross shape: N=8 L=1 S=2048 E=32 H=32, non-causal, bf16."""
+    """BASELINE cfg4's cross shape: N=8 L=1 S=2048 E=32 H=32, non-causal, bf16."""
     run(8, 1, 2048, 32, 32, torch.bfloat16, False, seed=12, device=cuda)
 
 
