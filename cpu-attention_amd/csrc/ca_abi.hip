@@ -106,13 +106,13 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
   const int64_t words = a->head_dim * esize(a->dtype) / 4;
 
   // The reference stores the new token, then attends (paged_attn.mojo:852-863).
-  // One token appended at lens (the serving step) is folded into the decode
-  // kernel: the wave whose tile holds position lens[s] writes it to the cache and
-  // attends it, so one launch does both (measured on MI355X: 8 x 16 rows fp32,
-  // 36.5 -> 31.7 us; 128 x 32 rows bf16, 238 -> 222 us).  Several tokens, or a
-  // store at given slots (which need not be the position the row attends), go
-  // through the store kernel first.
-  const bool fused = a->k_new && !a->slots && per_seq == 1;
+  // For a small batch, one token appended at lens (the serving step) is folded
+  // into the decode kernel: the wave whose tile holds position lens[s] writes it
+  // to the cache and attends it, so one launch does both.  Larger batches,
+  // several tokens, or a store at given slots (which need not be the position
+  // the row attends) go through the store kernel first.
+  const bool fused = a->k_new && !a->slots && per_seq == 1 &&
+                     a->num_seqs * a->num_heads <= kFusedAppendMaxRows;
   if (a->k_new && !fused) {
     StoreParams sp{};
     sp.key = static_cast<const uint32_t*>(a->k_new);

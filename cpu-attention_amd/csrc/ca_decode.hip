@@ -29,9 +29,13 @@
 //   P.V  lane groups of E/8 (bf16) or E/4 (fp32) lanes read whole V rows with
 //        16-byte loads; each wave instruction reads rows of G different units
 //        (pages), p comes from LDS.
-// K and V are read with non-temporal loads: each byte is used once (temporal loads
-// measured 13% slower on the bench's batch).  The one exception is K in a call that
-// appends a token (below).
+// K and V are read with non-temporal loads: each byte is used once.  (Measured on
+// MI355X: temporal loads for K and V made the bench's 1.1 GB batch 13% slower.
+// Temporal K loads in a call that appends a token made back-to-back calls on one
+// cache faster, since part of the cache then stays in the 256 MB MALL from one call
+// to the next, but made a call after a cache flush 11% slower: 4096 rows,
+// 287 against 258 us.  A model's other layers pass through the caches between two
+// steps of one layer, so the flushed case is the one kept.)
 #include <atomic>
 #include <mutex>
 
@@ -157,18 +161,14 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
   }
 
   // ---- the token appended by this call, at tile key newj.  Its words are read
-  // here (beside the page-table reads above, so the latencies overlap).  Its K
-  // words, 4 bytes in each of W lines (K is transposed in the page), are stored
-  // before the tile's K loads, and in append mode those loads are temporal: the
-  // lines then fill in L2 around the new words and go back to HBM whole, where a
-  // 4-byte write into a line the L2 does not hold costs the DRAM a read-modify-
-  // write (measured: 4096 rows per call, 238 us as a store kernel plus a decode,
-  // 222 us this way; with non-temporal K loads, 244 us).  The V row, a whole
-  // line, goes to the cache after the Q.K loop, ahead of the P.V loads that read
-  // it back (a workgroup-scope release and acquire orders the two for the wave's
-  // lanes; on gfx950 the CU keeps them in order and the fence costs nothing).
-  // The new key's logit, computed from the registers, replaces what the lane
-  // owning the key read from the slot.
+  // here (beside the page-table reads above, so the latencies overlap).  Right
+  // after the Q.K loop it goes to the cache: its K words land in lines the loop
+  // has just brought into L2 (4-byte writes into lines that are not resident
+  // would each cost the DRAM a read-modify-write), and its V row ahead of the
+  // P.V loads that read it back (a workgroup-scope release and acquire orders the
+  // two for the wave's lanes; on gfx950 the CU keeps them in order and the fence
+  // costs nothing).  Its logit, computed from the registers, replaces what the
+  // lane owning the key read from the slot.
   // Nothing is stored or substituted when the key's page names no block.
   constexpr int KNW = (W + kWave - 1) / kWave;  // K words of the new key per lane
   uint32_t knw[KNW], qnw[KNW];
@@ -187,18 +187,6 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
     vrow = lane < W / 4 ? *reinterpret_cast<const u32x4*>(vnew + 4 * lane) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  if (APPEND && newj >= 0) {
-    kbn = __shfl(kb, newj >> 4);
-    if (kbn >= 0) {
-      const int x = newj & (kUnit - 1);
-#pragma unroll
-      for (int i = 0; i < KNW; ++i) {
-        const int w = lane + kWave * i;
-        if (w < W) p.kc_store[kbn + (int64_t)w * p.page + x] = knw[i];
-      }
-    }
-  }
-
   // ---- Q.K: keys 4*lane .. 4*lane+3 of the tile.
   float s[4];
   {
@@ -214,9 +202,8 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
           u32x4 k4[UNROLL];
 #pragma unroll
           for (int i = 0; i < UNROLL; ++i)
-            k4[i] = APPEND ? *reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page)
-                           : __builtin_nontemporal_load(
-                                 reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page));
+            k4[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page));
 #pragma unroll
           for (int i = 0; i < UNROLL; ++i) {
             const bf16x2 qv = as_bf16x2(qw[w0 + i]);
@@ -236,9 +223,8 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
           u32x4 k4[UNROLL];
 #pragma unroll
           for (int i = 0; i < UNROLL; ++i)
-            k4[i] = APPEND ? *reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page)
-                           : __builtin_nontemporal_load(
-                                 reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page));
+            k4[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page));
 #pragma unroll
           for (int i = 0; i < UNROLL; ++i) {
             const float qv = qf[w0 + i];
@@ -262,9 +248,15 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
     s[3] = (ok && key0 + 3 < ntok) ? a3 : -INFINITY;
   }
   if (APPEND && newj >= 0) {
+    kbn = __shfl(kb, newj >> 4);
     const int64_t vbn = __shfl(vb, newj >> 4);
     if (kbn >= 0) {
       const int x = newj & (kUnit - 1);
+#pragma unroll
+      for (int i = 0; i < KNW; ++i) {
+        const int w = lane + kWave * i;
+        if (w < W) p.kc_store[kbn + (int64_t)w * p.page + x] = knw[i];
+      }
       if (lane < W / 4)
         *reinterpret_cast<u32x4*>(p.vc_store + (vbn + (int64_t)x * E) * ES / 4 + 4 * lane) = vrow;
     }

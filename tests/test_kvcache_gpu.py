@@ -51,14 +51,14 @@ def test_append_one_token(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("nseqs", [2, 129, 600])
-def test_append_in_the_decode_kernel(cuda, dtype, nseqs):
-    """One token appended per sequence is written and attended by the decode kernel
-    itself (one launch), from 16 rows to 4800: the cache holds the bytes the layout
-    oracle says (the unwritten slots keep their NaN poison) and the output attends
-    the new token.  Edge positions: an empty row, the last slot of a page, the first
-    slot of a new page, and a row past one block's 2048 keys, whose blocks meet in
-    the combine kernel."""
+@pytest.mark.parametrize("nseqs", [2, 128, 129, 600])
+def test_append_either_side_of_the_fused_limit(cuda, dtype, nseqs):
+    """One token appended per sequence, over 16 and 128 x 8 = 1024 rows inside the
+    decode kernel, over 129 x 8 = 1032 and 4800 rows by the store kernel first: the
+    cache holds the bytes the layout oracle says (the unwritten slots keep their NaN
+    poison) and the output attends the new token.  Edge positions: an empty row, the
+    last slot of a page, the first slot of a new page, and a row past one block's
+    2048 keys, whose blocks meet in the combine kernel."""
     h, d, page = 8, 64, 16
     rng = random.Random(nseqs)
     lens = [rng.randrange(0, 300) for _ in range(nseqs)]
