@@ -68,26 +68,44 @@ extern "C" int ca_store(const ca_store_args* a, void* stream) {
 }
 
 // Workspace layout: fp32 partial accumulators [slots, E], then (max, sum) pairs
-// [slots, 2], one slot per (row, 256-key tile of the page table's capacity).
+// [slots, 2], one slot per (row, block of 8 tiles of the page table's capacity).
 static int64_t decode_acc_bytes(int64_t slots, int64_t head_dim) {
   return ((slots * head_dim * 4 + 255) / 256) * 256;
+}
+
+static int64_t decode_ws_bytes(int64_t rows, int64_t head_dim, int64_t page, int64_t width, int tile_keys) {
+  const int64_t slots = decode_workspace_slots(rows, decode_tiles(width, page, tile_keys));
+  return decode_acc_bytes(slots, head_dim) + slots * 2 * 4;
 }
 
 extern "C" int64_t ca_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads,
                                              int64_t head_dim, int64_t page_size,
                                              int64_t page_table_width) {
   if (num_seqs < 0 || num_heads < 0 || page_size <= 0 || page_table_width < 0) return -1;
-  const int64_t slots = decode_workspace_slots(num_seqs * num_heads,
-                                               decode_tiles(page_table_width, page_size));
-  return decode_acc_bytes(slots, head_dim) + slots * 2 * 4;
+  const int64_t rows = num_seqs * num_heads;
+  return decode_ws_bytes(rows, head_dim, page_size, page_table_width,
+                         decode_tile_keys(rows, page_table_width, page_size, head_dim));
 }
 
-extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
+// ca_decode and ca_decode_noalloc.  noalloc: the split-K scratch is the library's
+// fixed buffer; a call whose partials with the usual tile size do not fit takes
+// 256-key tiles (fewer partials per row) if those fit.
+static int decode_entry(const ca_decode_args* a, void* stream, bool noalloc) {
   if (!a || !dtype_ok(a->dtype) || !head_dim_ok(a->head_dim) || !page_ok(a->page_size))
     return CA_DECLINED;
   if (a->num_seqs < 0 || a->num_heads <= 0 || a->num_blocks < 0 || a->page_table_width < 0)
     return CA_DECLINED;
   if (a->num_seqs == 0) return CA_OK;
+  // The tile size and the split-K scratch it needs depend on the shapes only; the
+  // no-allocation entry refuses a call its buffer cannot hold before anything else.
+  const int64_t rows = a->num_seqs * a->num_heads;
+  int tile_keys = decode_tile_keys(rows, a->page_table_width, a->page_size, a->head_dim);
+  int64_t need = decode_ws_bytes(rows, a->head_dim, a->page_size, a->page_table_width, tile_keys);
+  if (noalloc && need > CA_DECODE_NOALLOC_SCRATCH_BYTES && tile_keys != kDecodeLongTile) {
+    tile_keys = kDecodeLongTile;
+    need = decode_ws_bytes(rows, a->head_dim, a->page_size, a->page_table_width, tile_keys);
+  }
+  if (noalloc && need > CA_DECODE_NOALLOC_SCRATCH_BYTES) return CA_SCRATCH_EXCEEDED;
   if (!a->q || !a->k_cache || !a->v_cache || !a->lens || !a->page_table || !a->out)
     return CA_DECLINED;
   if ((a->k_new == nullptr) != (a->v_new == nullptr)) return CA_DECLINED;
@@ -99,12 +117,20 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
     return CA_DECLINED;
   if (a->k_new && (!aligned16(a->k_new) || !aligned16(a->v_new) || !stride16(a->kv_stride, a->dtype)))
     return CA_DECLINED;
-  const int64_t need = ca_decode_workspace_bytes(a->num_seqs, a->num_heads, a->head_dim,
-                                                 a->page_size, a->page_table_width);
-  if (need > 0 && (!a->workspace || !aligned16(a->workspace) || a->workspace_bytes < need)) return CA_DECLINED;
+  void* workspace = a->workspace;
+  int64_t workspace_bytes = a->workspace_bytes;
+  if (noalloc) {
+    workspace = nullptr;
+    workspace_bytes = 0;
+    if (need > 0) {
+      const int r = decode_noalloc_scratch(&workspace);
+      if (r != CA_OK) return r;
+      workspace_bytes = CA_DECODE_NOALLOC_SCRATCH_BYTES;
+    }
+  }
+  if (need > 0 && (!workspace || !aligned16(workspace) || workspace_bytes < need)) return CA_DECLINED;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t words = a->head_dim * esize(a->dtype) / 4;
-
   // The reference stores the new token, then attends (paged_attn.mojo:852-863).
   // For a small batch, one token appended at lens (the serving step) is folded
   // into the decode kernel: the wave whose tile holds position lens[s] writes it
@@ -149,11 +175,12 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
   p.nblocks = a->num_blocks;
   p.nseqs = a->num_seqs;
   p.c = a->scale * kLog2e;
-  p.tiles = (int)decode_tiles(a->page_table_width, a->page_size);
-  p.slots = decode_workspace_slots(a->num_seqs * a->num_heads, p.tiles);
+  p.tile_keys = tile_keys;
+  p.tiles = (int)decode_tiles(a->page_table_width, a->page_size, tile_keys);
+  p.slots = decode_workspace_slots(rows, p.tiles);
   const int64_t acc_bytes = decode_acc_bytes(p.slots, a->head_dim);
-  p.part_acc = static_cast<float*>(a->workspace);
-  p.part_ml = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + acc_bytes);
+  p.part_acc = static_cast<float*>(workspace);
+  p.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes);
   p.out = a->out;
   if (fused) {
     p.k_new = static_cast<const uint32_t*>(a->k_new);
@@ -165,21 +192,12 @@ extern "C" int ca_decode(const ca_decode_args* a, void* stream) {
   return decode_launch(p, (int)a->head_dim, a->dtype == CA_BF16, st);
 }
 
+
+extern "C" int ca_decode(const ca_decode_args* a, void* stream) { return decode_entry(a, stream, false); }
+
 extern "C" int ca_decode_noalloc(const ca_decode_args* a, void* stream) {
   static_assert(CA_DECODE_NOALLOC_SCRATCH_BYTES == (32ll << 20), "the status string names the size");
-  if (!a) return CA_DECLINED;
-  const int64_t need = ca_decode_workspace_bytes(a->num_seqs, a->num_heads, a->head_dim, a->page_size,
-                                                 a->page_table_width);
-  if (need > CA_DECODE_NOALLOC_SCRATCH_BYTES) return CA_SCRATCH_EXCEEDED;
-  ca_decode_args b = *a;
-  b.workspace = nullptr;
-  b.workspace_bytes = 0;
-  if (need > 0) {
-    const int r = decode_noalloc_scratch(&b.workspace);
-    if (r != CA_OK) return r;
-    b.workspace_bytes = CA_DECODE_NOALLOC_SCRATCH_BYTES;
-  }
-  return ca_decode(&b, stream);
+  return decode_entry(a, stream, true);
 }
 
 extern "C" int64_t ca_flash_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t num_heads,

@@ -1,4 +1,4 @@
-// Paged decode on CDNA4: split-K over 256-key tiles plus a combine pass.
+// Paged decode on CDNA4: split-K over 64- or 256-key tiles plus a combine pass.
 //
 // Follows the reference's decode (cpu_attention/_mojo/src/paged_attn.mojo:714-782):
 // logits q.k, base-2 online softmax with c = scale*log2(e) and the running max in
@@ -7,25 +7,27 @@
 // never read (0 * NaN would poison the row, :686-687), nor are page-table entries
 // past the last page in use.
 //
-// Work split.  One wave per 256-key tile of one row (sequence, head): grid.x walks
-// the rows, grid.y the tile groups (8 tiles, 2048 keys, per 512-thread block) up
-// to the page table's capacity, so every row's first tiles are dispatched first;
-// waves whose tile is past the row's length exit at once (a block barrier waits
-// only for the waves still running).  The waves of a block merge their partial
-// (max, sum, P.V) states in LDS: a row of up to 2048 keys is written by its one
-// block, with no workspace traffic and no second kernel.  Longer rows leave one
-// partial per block in the workspace, and the combine kernel merges those.  The
-// host needs no lengths and nothing synchronises.  (A stream-K split into equal
-// slices per resident wave was measured slower: 347 us against 189 us on the
-// bench's batch.)
+// Work split.  One wave per tile of one row (sequence, head): grid.x walks the
+// rows, grid.y the tile groups (8 tiles per 512-thread block: 512 keys of 64-key
+// tiles, 2048 of 256-key tiles) up to the page table's capacity, so every row's
+// first tiles are dispatched first.  decode_tile_keys (below) picks the tile size
+// from the call's shapes.  Waves whose tile is past the row's length exit at once
+// (a block barrier waits only for the waves still running).  The waves of a block
+// merge their partial (max, sum, P.V) states in LDS: a row that fits one block is
+// written by it, with no workspace traffic.  Longer rows leave one partial per
+// block in the workspace, and the combine kernel merges those.  The host needs no
+// lengths and nothing synchronises.  (A stream-K split into equal slices per
+// resident wave was measured slower: 347 us against 189 us on a 1.1 GB batch.)
 //
 // Layout use (the reference's PageLayout, :58-130): a 16-key unit never straddles a
 // page (P % 16 == 0), so a tile is up to 16 units, each one contiguous run inside one
 // (block, head):
-//   Q.K  lane l owns keys 4l..4l+3 of the tile; one 16-byte load per K word row
-//        (w*P + t .. t+3) gives those 4 keys' word w, so the dot product needs no
-//        cross-lane reduction.  bf16 words are dim pairs: v_dot2_f32_bf16 with the
-//        matching q pair (exact products, fp32 accumulation).
+//   Q.K  lane l owns keys 4l..4l+3 of a 256-key tile; one 16-byte load per K word
+//        row (w*P + t .. t+3) gives those 4 keys' word w, so the dot product needs
+//        no cross-lane reduction.  A 64-key tile gives each key quad to 4 lanes
+//        that take every 4th word and sum their partial products at the end.
+//        bf16 words are dim pairs: v_dot2_f32_bf16 with the matching q pair
+//        (exact products, fp32 accumulation).
 //   P.V  lane groups of E/8 (bf16) or E/4 (fp32) lanes read whole V rows with
 //        16-byte loads; each wave instruction reads rows of G different units
 //        (pages), p comes from LDS.
@@ -79,9 +81,11 @@ int decode_noalloc_scratch(void** ptr) {
   return CA_OK;
 }
 
-constexpr int kTile = 256;    // keys per tile
-constexpr int kUnit = 16;     // keys per unit (one page run)
-constexpr int kDecWaves = 8;  // tiles (waves) per block
+constexpr int kTile = kDecodeLongTile;  // keys per long tile
+constexpr int kShortTile = 64;           // keys per short tile
+constexpr int kUnit = 16;                // keys per unit (one page run)
+constexpr int kDecWaves = 8;             // tiles (waves) per block
+static_assert(kTile == 256, "long tiles: one key quad per lane");
 
 // out[idx .. idx+N) = v * inv in the output dtype (bf16: round to nearest even).
 template <int N, bool BF>
@@ -133,23 +137,35 @@ struct RowState {
   }
 };
 
-// Keys [t0, t0 + ntok) of row (seq, h): 0 < ntok <= 256, t0 % 16 == 0, t0 + ntok <= len.
-// Folds them into st.  p_lds is this wave's 256-float scratch.  newj >= 0 (wave-
+// Keys [t0, t0 + ntok) of row (seq, h): 0 < ntok <= TK, t0 % 16 == 0, t0 + ntok <= len.
+// Folds them into st.  p_lds is this wave's TK-float scratch.  newj >= 0 (wave-
 // uniform) names the key of the tile that is the token appended by this call: the
-// wave copies it from p.k_new / p.v_new into the cache before reading the tile.
-template <int E, bool BF, bool APPEND>
+// wave copies it from p.k_new / p.v_new into the cache.
+//
+// TK = 256: lane l owns the key quad l (keys 4l..4l+3) and all W words of it.
+// TK = 64: the 16 key quads of the tile are shared by SPLIT = 4 lanes each: lane l
+// takes quad l % 16 and words l / 16, l / 16 + 4, ..., and the four partial dot
+// products are summed across the lanes afterwards.
+template <int E, bool BF, bool APPEND, int TK>
 __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, int64_t h,
                                             int64_t t0, int ntok, int newj, float* p_lds,
                                             RowState<E, BF>& st) {
   using D = DecodeShape<E, BF>;
   constexpr int W = D::W, DPL = D::DPL, LPR = D::LPR, G = D::G, ES = D::ES, UNROLL = D::UNROLL;
+  constexpr int NU = TK / kUnit;           // units per tile
+  constexpr int NQ = TK / 4;               // key quads per tile
+  constexpr int SPLIT = kWave / NQ;        // lanes per key quad
+  constexpr int WPL = W / SPLIT;           // K words per lane
+  constexpr int QU = WPL < UNROLL ? WPL : UNROLL;  // K loads per batch
+  static_assert((TK == kTile || TK == kShortTile) && W % SPLIT == 0 && WPL % QU == 0, "tile shape");
   const int lane = threadIdx.x & 63;
+  const int quad = lane % NQ, phase = lane / NQ;
 
-  // Unit table: lane u < 16 resolves unit u's page once (word index of its K run,
+  // Unit table: lane u < NU resolves unit u's page once (word index of its K run,
   // element index of its V rows); -1 marks a unit past the tile or a page-table
   // entry that names no block.
   int64_t kb = -1, vb = -1;
-  if (lane < kTile / kUnit && kUnit * lane < ntok) {
+  if (lane < NU && kUnit * lane < ntok) {
     const int64_t tu = t0 + kUnit * lane;
     const int64_t pi = tu / p.page, off = tu - pi * p.page;
     const int64_t blk = p.page_table[seq * p.pt_width + pi];
@@ -187,26 +203,26 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
     vrow = lane < W / 4 ? *reinterpret_cast<const u32x4*>(vnew + 4 * lane) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  // ---- Q.K: keys 4*lane .. 4*lane+3 of the tile.
+  // ---- Q.K: keys 4*quad .. 4*quad+3 of the tile, words phase, phase + SPLIT, ...
   float s[4];
   {
-    const int64_t kbu = __shfl(kb, lane >> 2);
-    const int key0 = 4 * lane;
+    const int64_t kbu = __shfl(kb, quad >> 2);
+    const int key0 = 4 * quad;
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
     if (kbu >= 0 && key0 < ntok) {
-      const uint32_t* kp = p.kc + kbu + 4 * (lane & 3);
+      const uint32_t* kp = p.kc + kbu + 4 * (quad & 3) + (int64_t)phase * p.page;
       if constexpr (BF) {
         const uint32_t* qw = reinterpret_cast<const uint32_t*>(
-            reinterpret_cast<const uint16_t*>(p.q) + seq * p.q_stride + h * E);
-        for (int w0 = 0; w0 < W; w0 += UNROLL) {
-          u32x4 k4[UNROLL];
+            reinterpret_cast<const uint16_t*>(p.q) + seq * p.q_stride + h * E) + phase;
+        for (int w0 = 0; w0 < WPL; w0 += QU) {
+          u32x4 k4[QU];
 #pragma unroll
-          for (int i = 0; i < UNROLL; ++i)
+          for (int i = 0; i < QU; ++i)
             k4[i] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page));
+                reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * SPLIT * p.page));
 #pragma unroll
-          for (int i = 0; i < UNROLL; ++i) {
-            const bf16x2 qv = as_bf16x2(qw[w0 + i]);
+          for (int i = 0; i < QU; ++i) {
+            const bf16x2 qv = as_bf16x2(qw[(w0 + i) * SPLIT]);
             a0 = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(k4[i].x), qv, a0, false);
             a1 = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(k4[i].y), qv, a1, false);
             a2 = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(k4[i].z), qv, a2, false);
@@ -216,18 +232,18 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
       } else {
         // Four partial sums per key (words w mod 4): 32-term chains instead of one
         // 128-term chain keep the fp32 logits well inside the 1e-6 decode gate.
-        const float* qf = reinterpret_cast<const float*>(p.q) + seq * p.q_stride + h * E;
+        const float* qf = reinterpret_cast<const float*>(p.q) + seq * p.q_stride + h * E + phase;
         float c0[4] = {0.f, 0.f, 0.f, 0.f}, c1[4] = {0.f, 0.f, 0.f, 0.f};
         float c2[4] = {0.f, 0.f, 0.f, 0.f}, c3[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int w0 = 0; w0 < W; w0 += UNROLL) {
-          u32x4 k4[UNROLL];
+        for (int w0 = 0; w0 < WPL; w0 += QU) {
+          u32x4 k4[QU];
 #pragma unroll
-          for (int i = 0; i < UNROLL; ++i)
+          for (int i = 0; i < QU; ++i)
             k4[i] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * p.page));
+                reinterpret_cast<const u32x4*>(kp + (int64_t)(w0 + i) * SPLIT * p.page));
 #pragma unroll
-          for (int i = 0; i < UNROLL; ++i) {
-            const float qv = qf[w0 + i];
+          for (int i = 0; i < QU; ++i) {
+            const float qv = qf[(w0 + i) * SPLIT];
             c0[i & 3] = fmaf(__uint_as_float(k4[i].x), qv, c0[i & 3]);
             c1[i & 3] = fmaf(__uint_as_float(k4[i].y), qv, c1[i & 3]);
             c2[i & 3] = fmaf(__uint_as_float(k4[i].z), qv, c2[i & 3]);
@@ -238,6 +254,17 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
         a1 = (c1[0] + c1[1]) + (c1[2] + c1[3]);
         a2 = (c2[0] + c2[1]) + (c2[2] + c2[3]);
         a3 = (c3[0] + c3[1]) + (c3[2] + c3[3]);
+      }
+    }
+    if constexpr (SPLIT > 1) {
+      // The SPLIT lanes of a quad (lanes quad, quad + NQ, ...) sum their partial
+      // products; every one of them ends with the same four logits.
+#pragma unroll
+      for (int o = NQ; o < kWave; o <<= 1) {
+        a0 += __shfl_xor(a0, o);
+        a1 += __shfl_xor(a1, o);
+        a2 += __shfl_xor(a2, o);
+        a3 += __shfl_xor(a3, o);
       }
     }
     // Raw logits (masked keys -inf); the scale is folded into the exponent below.
@@ -271,7 +298,7 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
         part = fmaf(__uint_as_float(knw[i]), __uint_as_float(qnw[i]), part);
     }
     const float logit = wave_sum(part);
-    if (kbn >= 0 && lane == (newj >> 2)) {
+    if (kbn >= 0 && quad == (newj >> 2)) {
       const int j = newj & 3;
       s[0] = j == 0 ? logit : s[0];
       s[1] = j == 1 ? logit : s[1];
@@ -295,45 +322,51 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
     pr[j] = __builtin_amdgcn_exp2f(fmaf(s[j], p.c, -mu));
     ls += pr[j];
   }
-  st.l = fmaf(st.l, alpha, ls);
+  st.l = fmaf(st.l, alpha, phase == 0 ? ls : 0.f);  // one lane per quad counts it
 #pragma unroll
   for (int i = 0; i < DPL; ++i) st.acc[i] *= alpha;
   wave_lds_sync();  // the previous tile's P.V reads are done
-  *reinterpret_cast<f32x4*>(&p_lds[4 * lane]) = f32x4{pr[0], pr[1], pr[2], pr[3]};
+  if (phase == 0) *reinterpret_cast<f32x4*>(&p_lds[4 * quad]) = f32x4{pr[0], pr[1], pr[2], pr[3]};
   wave_lds_sync();
 
-  // ---- P.V: lane group g (of G) takes units g*UPG .. g*UPG+UPG-1 of the tile,
-  // lane dl of the group dims dl*DPL..  Load j of a lane reads row j / UPG of unit
-  // g*UPG + j % UPG, so one wave instruction spans G units and a batch of 16 loads
-  // spans every unit of the group: the reads fan out over many pages at once,
-  // which streams far better than walking one page row by row.
-  constexpr int UPG = kTile / kUnit / G;   // units per group
-  constexpr int R = kUnit * UPG;           // rows per lane
-  constexpr int B = R < 16 ? R : 16;       // loads in flight
+  // ---- P.V: lane group g (of G), lane dl of the group dims dl*DPL..
+  // 256-key tiles: group g takes units g*UPG .. g*UPG+UPG-1; load j of a lane reads
+  // row j / UPG of unit g*UPG + j % UPG, so one wave instruction spans G units and a
+  // batch of 16 loads spans every unit of the group: the reads fan out over many
+  // pages at once, which streams far better than walking one page row by row.
+  // 64-key tiles (4 units, G of 4 to 16 groups): load j of group g reads key
+  // g + G*j, so one wave instruction reads G consecutive rows of one unit (the unit
+  // is the same for every lane, since G divides 16) and a batch spans all 4 units.
+  constexpr bool BY_UNIT = NU >= G;
+  constexpr int UPG = BY_UNIT ? NU / G : 1;  // units per group (256-key tiles)
+  constexpr int NV = BY_UNIT ? UPG : NU;     // unit bases a lane holds
+  constexpr int R = TK / G;                  // rows per lane
+  constexpr int B = R < 16 ? R : 16;         // loads in flight
   const int g = lane / LPR, dl = lane - g * LPR;
-  int64_t vbu[UPG];
+  int64_t vbu[NV];
 #pragma unroll
-  for (int k = 0; k < UPG; ++k) vbu[k] = __shfl(vb, g * UPG + k);
+  for (int k = 0; k < NV; ++k) vbu[k] = __shfl(vb, BY_UNIT ? g * UPG + k : k);
+  // Load j: its key in the tile, and which of the lane's unit bases holds it.
+  auto key_of = [&](int j) { return BY_UNIT ? kUnit * (g * UPG + j % UPG) + j / UPG : g + G * j; };
+  auto base_of = [&](int j) { return BY_UNIT ? j % UPG : G * j / kUnit; };
   const char* vbase = reinterpret_cast<const char*>(p.vc) + dl * 16;
-  const int t_first = kUnit * g * UPG;     // this group's first token in the tile
 #pragma unroll
   for (int b0 = 0; b0 < R; b0 += B) {
-    if (t_first + b0 / UPG >= ntok) break;  // nothing left for this group
+    if (key_of(b0) >= ntok) break;  // the batch's first key (its smallest) is past the tile
     u32x4 v4[B];
     bool ok[B];
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const int j = b0 + i, k = j % UPG, x = j / UPG;
-      ok[i] = vbu[k] >= 0 && t_first + kUnit * k + x < ntok;
+      const int j = b0 + i, key = key_of(j), k = base_of(j);
+      ok[i] = vbu[k] >= 0 && key < ntok;
       if (ok[i])
         v4[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(vbase + (vbu[k] + (int64_t)x * E) * ES));
+            reinterpret_cast<const u32x4*>(vbase + (vbu[k] + (int64_t)(key & (kUnit - 1)) * E) * ES));
     }
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const int j = b0 + i, k = j % UPG, x = j / UPG;
       if (ok[i]) {
-        const float pj = p_lds[t_first + kUnit * k + x];
+        const float pj = p_lds[key_of(b0 + i)];
         const u32x4 v = v4[i];
         if constexpr (BF) {
           st.acc[0] = fmaf(pj, bf16_lo(v.x), st.acc[0]);
@@ -399,19 +432,19 @@ __device__ __forceinline__ float merge_states(int n, Get&& get, float& mx, float
   return l;
 }
 
-// One wave per 256-key tile of each row, 8 tiles per block merged in LDS.
+// One wave per TK-key tile of each row, 8 tiles per block merged in LDS.
 // APPEND: the call's one-token append is done here (p.k_new).
-template <int E, bool BF, bool APPEND>
+template <int E, bool BF, bool APPEND, int TK>
 __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(4)))
 void decode_tiles_kernel(DecodeParams p) {
-  __shared__ __attribute__((aligned(16))) float p_lds[kDecWaves][kTile];
+  __shared__ __attribute__((aligned(16))) float p_lds[kDecWaves][TK];
   __shared__ float part[kDecWaves][E + 2];
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t row = blockIdx.x;
   const int64_t s = row / p.heads, h = row - s * p.heads;
   const int64_t tile = (int64_t)blockIdx.y * kDecWaves + wv;
   const int64_t len = row_len(p, s);
-  const int64_t t0 = tile * kTile;
+  const int64_t t0 = tile * TK;
   // Waves past the row's end exit (whole waves: the barrier below waits for the
   // others only), except the first wave of the row, which writes a row with no
   // key as exactly 0.
@@ -423,20 +456,20 @@ void decode_tiles_kernel(DecodeParams p) {
   int newj = -1;
   if (APPEND) {
     const int64_t pos = p.lens[s];
-    if (pos >= t0 && pos < t0 + kTile && pos < len) newj = (int)(pos - t0);
+    if (pos >= t0 && pos < t0 + TK && pos < len) newj = (int)(pos - t0);
   }
-  if (t0 < len) decode_tile<E, BF, APPEND>(p, s, h, t0, (int)min<int64_t>(kTile, len - t0), newj, p_lds[wv], st);
+  if (t0 < len) decode_tile<E, BF, APPEND, TK>(p, s, h, t0, (int)min<int64_t>(TK, len - t0), newj, p_lds[wv], st);
   wave_partial<E, BF>(st, part[wv]);
   __syncthreads();
   if (wv != 0) return;
   constexpr int DPC = E >= 64 ? E / 64 : 1;
   const int lane = threadIdx.x & 63;
-  const int n = (int)max<int64_t>(1, min<int64_t>(kDecWaves, cdiv(len, kTile) - (int64_t)blockIdx.y * kDecWaves));
+  const int n = (int)max<int64_t>(1, min<int64_t>(kDecWaves, cdiv(len, TK) - (int64_t)blockIdx.y * kDecWaves));
   float mx, acc[DPC];
   const float l = merge_states<E, DPC>(n, [&](int t, int i) {
     return part[t][i == -1 ? E : (i == -2 ? E + 1 : i)];
   }, mx, acc);
-  if (blockIdx.y == 0 && len <= kDecWaves * kTile) {
+  if (blockIdx.y == 0 && len <= kDecWaves * TK) {
     if (lane * DPC < E) store_out<DPC, BF>(p.out, row * E + lane * DPC, acc, l > 0.f ? 1.f / l : 0.f);
   } else {
     const int64_t slot = row * cdiv(p.tiles, kDecWaves) + blockIdx.y;
@@ -459,18 +492,39 @@ __global__ __launch_bounds__(256) void decode_tiles_combine_kernel(DecodeParams 
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= p.nseqs * p.heads) return;
   const int64_t len = row_len(p, row / p.heads);
-  if (len <= kDecWaves * kTile) return;  // written by its block
+  const int64_t span = (int64_t)kDecWaves * p.tile_keys;  // keys per block
+  if (len <= span) return;  // written by its block
   const int64_t nb = cdiv(p.tiles, kDecWaves);
   const float* ml = p.part_ml + row * nb * 2;
   const float* pa = p.part_acc + row * nb * E;
   float mx, acc[DPC];
-  const float l = merge_states<E, DPC>((int)cdiv(len, kDecWaves * kTile), [&](int t, int i) {
+  const float l = merge_states<E, DPC>((int)cdiv(len, span), [&](int t, int i) {
     return i == -1 ? ml[2 * t] : (i == -2 ? ml[2 * t + 1] : pa[t * E + i]);
   }, mx, acc);
   if (lane * DPC < E) store_out<DPC, BF>(p.out, row * E + lane * DPC, acc, l > 0.f ? 1.f / l : 0.f);
 }
 
-int64_t decode_tiles(int64_t pt_width, int64_t page) { return cdiv(pt_width * page, kTile); }
+// Tile size of a call.  64-key tiles give a row four times the waves of 256-key
+// tiles, each with a quarter of the serial load batches (one K batch, one V batch),
+// so more loads are in flight per CU; measured on MI355X with flushed caches they
+// win from batch-1 decode (N=1 H=32 E=128, 4096 keys: 41 -> 23 us) up to the
+// largest batches (N=64 H=32 E=128, lengths 17..2047: 196 -> 185 us; N=64 H=16
+// E=128 fp32: 276 -> 208 us).  They lose where every row fits one 256-key block
+// (2048 keys, so no combine pass), those blocks already give every CU one (256
+// rows or more), and the call is small: there the combine launch the 64-key
+// tiles need costs more than they save
+// (N=8 H=32 E=64, 2048 keys: 18.2 -> 21.9 us; N=8 H=32 E=32: 16.3 -> 19.2 us).
+// The rule depends on shapes only (not on lengths or dtype), so the workspace size
+// does too.
+int decode_tile_keys(int64_t rows, int64_t pt_width, int64_t page, int64_t head_dim) {
+  const int64_t cap = pt_width * page;
+  const bool one_block = cap <= (int64_t)kDecWaves * kTile;
+  const bool fills = rows >= 256;
+  const bool small = rows * cap * head_dim <= (80ll << 20);  // K elements at capacity
+  return one_block && fills && small ? kTile : kShortTile;
+}
+
+int64_t decode_tiles(int64_t pt_width, int64_t page, int tile_keys) { return cdiv(pt_width * page, tile_keys); }
 
 // Partial slots the workspace must hold: one per (row, block of 8 tiles) when
 // rows can outgrow one block, none otherwise.
@@ -478,17 +532,26 @@ int64_t decode_workspace_slots(int64_t rows, int64_t tiles) {
   return tiles > kDecWaves ? rows * cdiv(tiles, kDecWaves) : 0;
 }
 
+template <int E, bool BF, bool APPEND, int TK>
+static void decode_tiles_launch(const DecodeParams& p, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((decode_tiles_kernel<E, BF, APPEND, TK>), grid, dim3(64 * kDecWaves), 0, stream, p);
+}
+
 template <int E, bool BF>
 static int decode_launch_t(const DecodeParams& p, hipStream_t stream) {
   const int64_t rows = p.nseqs * p.heads;
   const int64_t gy = cdiv(p.tiles, kDecWaves);
-  if (rows > 0x7fffffff || gy > 65535 || decode_workspace_slots(rows, p.tiles) > p.slots) return CA_DECLINED;
-  if (p.k_new)
-    hipLaunchKernelGGL((decode_tiles_kernel<E, BF, true>), dim3((unsigned)rows, (unsigned)gy), dim3(64 * kDecWaves),
-                       0, stream, p);
+  if (rows > 0x7fffffff || gy > 65535 || decode_workspace_slots(rows, p.tiles) > p.slots ||
+      (p.tile_keys != kTile && p.tile_keys != kShortTile))
+    return CA_DECLINED;
+  const dim3 grid((unsigned)rows, (unsigned)gy);
+  const bool append = p.k_new != nullptr;
+  if (p.tile_keys == kShortTile)
+    append ? decode_tiles_launch<E, BF, true, kShortTile>(p, grid, stream)
+           : decode_tiles_launch<E, BF, false, kShortTile>(p, grid, stream);
   else
-    hipLaunchKernelGGL((decode_tiles_kernel<E, BF, false>), dim3((unsigned)rows, (unsigned)gy), dim3(64 * kDecWaves),
-                       0, stream, p);
+    append ? decode_tiles_launch<E, BF, true, kTile>(p, grid, stream)
+           : decode_tiles_launch<E, BF, false, kTile>(p, grid, stream);
   int st = ca_launch_status();
   if (st != CA_OK || gy == 1) return st;
   hipLaunchKernelGGL((decode_tiles_combine_kernel<E, BF>), dim3((unsigned)cdiv(rows, 4)), dim3(256),

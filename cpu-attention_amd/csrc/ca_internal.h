@@ -32,7 +32,8 @@ struct DecodeParams {
   int64_t pt_width;
   int64_t heads, page, nblocks, nseqs;
   float c;                // softmax scale * log2(e)
-  int tiles;              // 256-key tiles per row at the page table's capacity
+  int tiles;              // tiles per row at the page table's capacity
+  int tile_keys;          // keys per tile: 256, or 64 for a batch too small to fill the GPU
   int64_t slots;          // partial slots the workspace holds
   float* part_acc;        // [slots, E]
   float* part_ml;         // [slots, 2]: running max (scaled log2 units), sum
@@ -82,7 +83,9 @@ constexpr int64_t kRowsMaxSplits = 64;
 constexpr int64_t kFusedAppendMaxRows = 1024;
 
 int store_launch(const StoreParams& p, int words, hipStream_t stream);
-int64_t decode_tiles(int64_t pt_width, int64_t page);
+constexpr int kDecodeLongTile = 256;  // keys per tile of the decode's long tiles
+int decode_tile_keys(int64_t rows, int64_t pt_width, int64_t page, int64_t head_dim);
+int64_t decode_tiles(int64_t pt_width, int64_t page, int tile_keys);
 int64_t decode_workspace_slots(int64_t rows, int64_t tiles);
 int decode_launch(const DecodeParams& p, int head_dim, int bf16, hipStream_t stream);
 int decode_noalloc_scratch(void** ptr);

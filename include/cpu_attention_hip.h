@@ -140,10 +140,12 @@ int ca_decode(const ca_decode_args* args, void* stream);
  * is a fixed device array inside the library, CA_DECODE_NOALLOC_SCRATCH_BYTES
  * (32 MiB) per GPU, held from the first call on that GPU until the process
  * ends; its address is resolved once per device (the current device at the
- * call; `stream` must belong to it).  A call whose
- * ca_decode_workspace_bytes(...) exceeds that size returns CA_SCRATCH_EXCEEDED
- * and enqueues nothing (32 MiB covers, e.g., 4096 rows of E=128 up to 30,720
- * keys of page-table capacity; rows of up to 2048 keys need none).  Every call
+ * call; `stream` must belong to it).  A call whose ca_decode_workspace_bytes(...)
+ * exceeds that size runs with 256-key tiles (fewer partials per row; its output
+ * may then differ from ca_decode's in the last bits, within the same tolerance);
+ * if those still do not fit, it returns CA_SCRATCH_EXCEEDED and enqueues nothing
+ * (32 MiB covers, e.g., 4096 rows of E=128 up to 30,720 keys of page-table
+ * capacity; rows of up to 2048 keys need none).  Every call
  * on a GPU shares that GPU's one buffer: calls that overlap on one GPU (two
  * streams, or two host threads) race on it and must be serialised by the
  * caller.  The buffer needs no clearing: each call writes every partial it

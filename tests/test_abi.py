@@ -91,23 +91,33 @@ def test_entries_decline_malformed_calls_without_a_gpu():
     d.dtype = 1
     assert lib.ca_decode(ctypes.byref(d), None) == K.CA_DECLINED  # null pointers
     # the no-allocation decode: a call whose split-K scratch exceeds the fixed buffer
-    # is refused before anything is enqueued (no GPU needed to see it)
-    d.dtype, d.page_table_width = 1, 4033  # 4033 pages of 16 keys: 32 blocks per row
+    # even with 256-key tiles (32 blocks of 2048 keys per row, 2048 rows: 34 MB of
+    # partials) is refused before anything is enqueued (no GPU needed to see it);
+    # one 233 pages narrower fits with 256-key tiles, so it gets as far as the
+    # pointer checks, although its usual 64-key tiles would need 126 MB
+    d.dtype, d.page_table_width = 1, 4033
     d.num_seqs, d.num_heads, d.head_dim = 64, 32, 128
-    need = lib.ca_decode_workspace_bytes(64, 32, 128, 16, 4033)
-    assert need > 32 << 20
+    assert lib.ca_decode_workspace_bytes(64, 32, 128, 16, 4033) > 32 << 20
     assert lib.ca_decode_noalloc(ctypes.byref(d), None) == K.CA_SCRATCH_EXCEEDED
-    assert lib.ca_decode_workspace_bytes(64, 32, 128, 16, 3800) <= 32 << 20
+    d.page_table_width = 3800
+    assert lib.ca_decode_workspace_bytes(64, 32, 128, 16, 3800) > 32 << 20
+    assert lib.ca_decode_noalloc(ctypes.byref(d), None) == K.CA_DECLINED  # null pointers
     assert lib.ca_decode_noalloc(None, None) == K.CA_DECLINED
     f = K.FlashArgs(batch=1, seq_q=0, seq_k=4, num_heads=1, head_dim=64, dtype=1)
     assert lib.ca_flash(ctypes.byref(f), None) == K.CA_DECLINED  # seq_q < 1
     f.seq_q = 4
     assert lib.ca_flash(ctypes.byref(f), None) == K.CA_DECLINED  # null pointers
-    # decode: one (max, sum, P.V) partial per (row, block of 8 tiles of 256 keys), and
-    # none when a row fits one block (2048 keys)
-    assert lib.ca_decode_workspace_bytes(64, 32, 128, 32, 64) == 0
-    assert lib.ca_decode_workspace_bytes(64, 32, 128, 32, 65) == \
-        ((64 * 32 * 2 * 128 * 4 + 255) // 256) * 256 + 64 * 32 * 2 * 2 * 4
+    # decode: one (max, sum, P.V) partial per (row, block of 8 tiles), none when a row
+    # fits one block.  Tiles are 64 keys (512 per block) unless every row fits one
+    # block of 256-key tiles (2048 keys), there are 256 rows or more, and K holds at
+    # most 80 Mi elements at the page table's capacity.
+    def partials(rows, blocks, d):
+        return ((rows * blocks * d * 4 + 255) // 256) * 256 + rows * blocks * 2 * 4
+    assert lib.ca_decode_workspace_bytes(8, 32, 64, 32, 64) == 0          # 256-key tiles
+    assert lib.ca_decode_workspace_bytes(64, 32, 128, 32, 64) == partials(2048, 4, 128)
+    assert lib.ca_decode_workspace_bytes(4, 32, 64, 32, 64) == partials(128, 4, 64)  # < 256 rows
+    assert lib.ca_decode_workspace_bytes(8, 32, 64, 32, 65) == partials(256, 5, 64)  # > 2048 keys
+    assert lib.ca_decode_workspace_bytes(1, 32, 128, 16, 32) == 0          # 512 keys: one block
     assert lib.ca_flash_workspace_bytes(1, 1, 1, 1, 64, 1) == 0
 
 

@@ -81,6 +81,42 @@ def test_append_either_side_of_the_fused_limit(cuda, dtype, nseqs):
     np.testing.assert_array_equal(cache_words(vc), vw)
 
 
+def long_tile_waves(nseqs, h, width, page):
+    """256-key tiles the decode's rows hold at the page table's capacity; the kernel
+    takes 64-key tiles when this is at most 2048 (csrc/ca_decode.hip)."""
+    return nseqs * h * -(-width * page // 256)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("tiles", ["short", "long"])
+def test_both_tile_sizes(cuda, dtype, d, tiles):
+    """A batch on each side of the 64/256-key tile choice, with rows at the edges of
+    tiles and of blocks (512 keys of 64-key tiles, 2048 of 256-key tiles) and rows
+    that span several blocks and meet in the combine kernel: a one-token append
+    attended in the same call, then a plain decode of the same cache."""
+    page = 16
+    if tiles == "short":
+        h, lens = 2, [0, 63, 64, 511, 512, 513, 1100, 3000]
+    else:
+        h, rng = 8, random.Random(d)
+        lens = [0, 255, 256, 2047, 2048, 2049, 2100] + [rng.randrange(0, 2101) for _ in range(57)]
+    # staged with one token more than lens, so that position lens[s] lies in a page of
+    # sequence s; the append overwrites that token
+    q, kc, vc, bt, ks, vs = stage([n + 1 for n in lens], h, d, page, dtype, seed=d, device=cuda)
+    waves = long_tile_waves(len(lens), h, bt.shape[1], page)
+    assert (waves <= 2048) == (tiles == "short")
+    ks, vs = [k[:, :n] for k, n in zip(ks, lens)], [v[:, :n] for v, n in zip(vs, lens)]
+    g = torch.Generator().manual_seed(d)
+    kn, vn = (torch.randn(len(lens), 1, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    out = flash_attn_with_kvcache(q, kc, vc, k=kn, v=vn, cache_seqlens=seqlens, page_table=bt)
+    ref = reference(q, *appended(ks, vs, kn, vn), d ** -0.5)
+    assert_close(out, ref, dtype, paged=True)
+    again = flash_attn_with_kvcache(q, kc, vc, cache_seqlens=seqlens + 1, page_table=bt)
+    assert_close(again, ref, dtype, paged=True)
+
+
 @pytest.mark.parametrize("host_checks", [True, False])
 def test_uneven_lengths(cuda, host_checks):
     """Lopsided batches (the reference sweeps thread counts here; the GPU splits every

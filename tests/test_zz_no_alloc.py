@@ -2,8 +2,9 @@
 is a fixed per-GPU buffer inside the library) against ca_decode with a caller
 workspace, through the C ABI: two calls in a row, the second with a smaller
 batch and page table, each bit-equal to ca_decode's output and within the
-decode gates of the float64 oracle; a call past the buffer's size is refused
-without touching the output."""
+decode gates of the float64 oracle; a call whose usual tile size needs more
+scratch than the buffer holds, on 256-key tiles; a call past the buffer's size
+even then is refused without touching the output."""
 
 import ctypes
 
@@ -56,6 +57,29 @@ def test_noalloc_matches_decode_on_two_calls(cuda, dtype):
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.uint8), ref_out.view(torch.uint8))
         assert_close(out, reference(q, ks, vs, d ** -0.5), dtype, paged=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_noalloc_takes_long_tiles_when_short_ones_do_not_fit(cuda, dtype):
+    """A batch whose 64-key-tile partials need more than the 32 MiB buffer (1024
+    rows, a page table of 40,960 keys) runs with 256-key tiles, whose partials fit,
+    and matches the float64 oracle; rows past 2048 keys use the combine kernel."""
+    lib = K.module().lib
+    h, d, page, width = 32, 128, 16, 2560
+    rng = np.random.default_rng(5)
+    lens = [2047, 2048, 2049, 5000] + rng.integers(17, 300, size=28).tolist()
+    print(f"noalloc long tiles dtype={dtype}", flush=True)
+    assert lib.ca_decode_workspace_bytes(len(lens), h, d, page, width) > 32 << 20
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=5, device=cuda)
+    # widen the page table to `width`: the entries past each row's pages name the
+    # helper's poisoned padding block, which the kernel never reads
+    table = torch.cat([bt, bt[:, -1:].expand(-1, width - bt.shape[1])], dim=1).contiguous()
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    out = torch.full_like(q, float("nan"))
+    rc = lib.ca_decode_noalloc(ctypes.byref(args_for(q, kc, vc, seqlens, table, out)), stream())
+    assert rc == K.CA_OK, lib.ca_status_string(rc)
+    torch.cuda.synchronize()
+    assert_close(out, reference(q, ks, vs, d ** -0.5), dtype, paged=True)
 
 
 def test_noalloc_refuses_past_its_buffer(cuda):
