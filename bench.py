@@ -74,12 +74,14 @@ CPU_BUDGET_S = 8.0  # seconds of back-to-back calls per CPU baseline
 METRIC = "decode HBM GB/s + µs/call; prefill TFLOP/s (bf16) vs MI355X roofline"
 
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of --profile-pass on
-# MI355X: the calibration copy, then the fifth of five calls of the decode and the
-# prefill kernel.
+# MI355X: the fifth of five calls of each workload (a decode call is its decode
+# and combine dispatches), and what the same counter read for the run's 1 GiB
+# calibration copy.
 TRAFFIC = {
-    "copy": {"fetch_kib": 524315.375, "write_kib": 1048576.0},
-    "decode": {"fetch_kib": 543394.5, "write_kib": 512.0},
-    "prefill": {"fetch_kib": 313687.062, "write_kib": 152576.0},
+    "decode": {"fetch_kib": 543080.5 + 1278.0, "write_kib": 2630.125 + 400.0,
+               "copy_fetch_kib": 524315.438, "copy_write_kib": 1048576.0},
+    "prefill": {"fetch_kib": 313687.062, "write_kib": 152576.0,
+                "copy_fetch_kib": 524315.375, "copy_write_kib": 1048576.0},
 }
 
 # The reference's published CPU figures (medians at its Python API, L2/L3 flushed,
@@ -108,8 +110,8 @@ def traffic_bytes(name):
     """HBM bytes of one call: each counter scaled by its reading for a known copy."""
     if name not in TRAFFIC:
         return None
-    t, c = TRAFFIC[name], TRAFFIC["copy"]
-    return int(t["fetch_kib"] * COPY_BYTES / c["fetch_kib"] + t["write_kib"] * COPY_BYTES / c["write_kib"])
+    t = TRAFFIC[name]
+    return int(t["fetch_kib"] * COPY_BYTES / t["copy_fetch_kib"] + t["write_kib"] * COPY_BYTES / t["copy_write_kib"])
 
 
 # ---------------------------------------------------------------------------
@@ -607,7 +609,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs_kernel, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs_kernel / HBM_PEAK_GBS, 4),
                      "traffic": traffic_bytes("decode"),
-                     "kernel": "decode_tiles_kernel<128,bf16> (one call: rows of up to 2048 keys merge in-block)",
+                     "kernel": "decode_tiles_kernel<128,bf16,64-key tiles> + decode_tiles_combine_kernel "
+                               "(the call's two dispatches, timed together)",
                      "algorithmic_bytes": w["bytes"]},
     }
     del w
