@@ -484,24 +484,57 @@ void decode_tiles_kernel(DecodeParams p) {
   }
 }
 
-// One wave per row longer than one block: merges the blocks' partials.
+// One wave per row longer than one block: merges the blocks' partials.  The
+// partials are read C at a time, every load of a round issued before any is used
+// (the kernel is latency-bound: a row has a few KB of partials); rounds merge
+// online.  A row of at most C blocks merges in one round, with the same
+// arithmetic as a single pass (weights 2^(m_t - M) against the row's max M).
 template <int E, bool BF>
 __global__ __launch_bounds__(256) void decode_tiles_combine_kernel(DecodeParams p) {
   constexpr int DPC = E >= 64 ? E / 64 : 1;
+  constexpr int C = 8;
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= p.nseqs * p.heads) return;
   const int64_t len = row_len(p, row / p.heads);
   const int64_t span = (int64_t)kDecWaves * p.tile_keys;  // keys per block
   if (len <= span) return;  // written by its block
   const int64_t nb = cdiv(p.tiles, kDecWaves);
+  const int n = (int)cdiv(len, span);
+  const bool dims = lane * DPC < E;
   const float* ml = p.part_ml + row * nb * 2;
-  const float* pa = p.part_acc + row * nb * E;
-  float mx, acc[DPC];
-  const float l = merge_states<E, DPC>((int)cdiv(len, span), [&](int t, int i) {
-    return i == -1 ? ml[2 * t] : (i == -2 ? ml[2 * t + 1] : pa[t * E + i]);
-  }, mx, acc);
-  if (lane * DPC < E) store_out<DPC, BF>(p.out, row * E + lane * DPC, acc, l > 0.f ? 1.f / l : 0.f);
+  const float* pa = p.part_acc + row * nb * E + (dims ? lane * DPC : 0);
+  float m = -INFINITY, l = 0.f, acc[DPC];
+#pragma unroll
+  for (int i = 0; i < DPC; ++i) acc[i] = 0.f;
+  for (int t0 = 0; t0 < n; t0 += C) {
+    float mt[C], lt[C], at[C][DPC];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const bool in = t0 + c < n;
+      mt[c] = in ? ml[2 * (t0 + c)] : -INFINITY;
+      lt[c] = in ? ml[2 * (t0 + c) + 1] : 0.f;
+#pragma unroll
+      for (int i = 0; i < DPC; ++i) at[c][i] = in && dims ? pa[(int64_t)(t0 + c) * E + i] : 0.f;
+    }
+    float mc = m;
+#pragma unroll
+    for (int c = 0; c < C; ++c) mc = fmaxf(mc, mt[c]);
+    if (mc == -INFINITY) continue;  // nothing readable yet
+    const float sc = __builtin_amdgcn_exp2f(m - mc);  // 0 on the first readable round
+    l *= sc;
+#pragma unroll
+    for (int i = 0; i < DPC; ++i) acc[i] *= sc;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const float w = __builtin_amdgcn_exp2f(mt[c] - mc);
+      l = fmaf(w, lt[c], l);
+#pragma unroll
+      for (int i = 0; i < DPC; ++i) acc[i] = fmaf(w, at[c][i], acc[i]);
+    }
+    m = mc;
+  }
+  if (dims) store_out<DPC, BF>(p.out, row * E + lane * DPC, acc, l > 0.f ? 1.f / l : 0.f);
 }
 
 // Tile size of a call.  64-key tiles give a row four times the waves of 256-key
