@@ -323,13 +323,207 @@ __global__ __launch_bounds__(64 * kRowsWaves) void flash_rows_kernel(FlashParams
   }
 }
 
+// Single-row calls whose heads lie side by side (head stride E in q, k and v, as
+// in a [batch, seq, heads, E] tensor or a fused projection) and short key ranges:
+// a wave instruction reads one key's HP = 64/G consecutive heads, 1 KB in one
+// run, instead of KPI keys of one head, KPI runs of E*esize bytes a token stride
+// apart, and the keys of a (batch, head group) are split over several blocks, so
+// many rows with few keys still give every wave a few chunks to stream (the
+// per-head route gives such a row one block of 8 waves with one chunk each).
+// Block = kRowsWaves waves on (batch, group of HP heads, split of the
+// keys); lane (hl, sl) holds head h0 + hl, slice sl; wave w takes chunks of
+// NSTEP keys sp*W + w, + W*splits, ..., with NBUF chunks in flight.  The numerics
+// are flash_rows_kernel's.
+template <int E, bool BF>
+struct HeadsShape {
+  static constexpr int ES = BF ? 2 : 4;    // element bytes
+  static constexpr int DPL = 16 / ES;      // elements per lane slice
+  static constexpr int G = E / DPL;        // lanes per head
+  static constexpr int HP = kWave / G;     // heads per load instruction
+  static constexpr int NSTEP = 4;          // keys per chunk (one load instruction each for K and V)
+  static constexpr int NBUF = 4;           // chunks in flight per wave
+};
+
+__host__ __device__ inline int rows_heads_per_load(int E, bool bf16) { return kWave / (E / (bf16 ? 8 : 4)); }
+
+// Splits of each (batch, head group)'s keys across blocks.
+__host__ __device__ inline int64_t rows_heads_splits(int64_t batch, int64_t seq_k, int64_t heads, int E, bool bf16) {
+  const int64_t blocks = batch * (heads / rows_heads_per_load(E, bf16));
+  const int64_t chunk_rounds = cdiv(cdiv(seq_k, 4), kRowsWaves);
+  int64_t s = blocks >= kRowsTargetBlocks ? 1 : cdiv(kRowsTargetBlocks, blocks);
+  s = s < chunk_rounds ? s : chunk_rounds;
+  s = s < kRowsMaxSplits ? s : kRowsMaxSplits;
+  return s < 1 ? 1 : s;
+}
+
+// The call takes flash_rows_heads_kernel: one query row, packed heads, a head
+// count the loads divide, and at most kRowsHeadsMaxKeys keys.  Measured on
+// MI355X with flushed caches against the per-head route: N=64 H=32 E=32 bf16,
+// 512 keys, 44.8 -> 29.8 us; 1024 keys (N=32 H=16) 23.0 -> 22.9 us; past that the
+// per-head route, which needs no combine pass at these batch sizes, is as fast or
+// faster (N=8 H=32 E=32, 2048 keys: 23.5 against 24.2 us).
+constexpr int64_t kRowsHeadsMaxKeys = 1024;
+__host__ __device__ inline bool rows_heads_shapes(int64_t seq_q, int64_t seq_k, int64_t heads, int E, bool bf16) {
+  return seq_q == 1 && seq_k <= kRowsHeadsMaxKeys && heads % rows_heads_per_load(E, bf16) == 0;
+}
+__host__ __device__ inline bool rows_heads_route(const FlashParams& p, int E, bool bf16) {
+  return rows_heads_shapes(p.seq_q, p.seq_k, p.heads, E, bf16) && p.qs[2] == E && p.ks[2] == E && p.vs[2] == E;
+}
+
+template <int E, bool BF>
+__global__ __launch_bounds__(64 * kRowsWaves) void flash_rows_heads_kernel(FlashParams p) {
+  using S = HeadsShape<E, BF>;
+  constexpr int DPL = S::DPL, G = S::G, HP = S::HP, W = kRowsWaves, NSTEP = S::NSTEP, NBUF = S::NBUF;
+  constexpr int PS = E + 2;  // floats per partial: acc[E], m, l
+  __shared__ float part[W][HP][PS];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t ng = p.heads / HP;
+  const int64_t lb = gridDim.y == 1 ? xcd_remap(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
+  const int64_t b = lb / ng, h0 = (lb - b * ng) * HP;
+  const int64_t splits = gridDim.y, sp = blockIdx.y;
+  const int sl = lane % G;   // this lane's slice of a head row
+  const int hl = lane / G;   // this lane's head within the group
+  const int64_t S_ = p.seq_k;
+  const int64_t nch = cdiv(S_, NSTEP);
+
+  const char* qb = static_cast<const char*>(p.q) + (b * p.qs[0] + (h0 + hl) * E + sl * DPL) * S::ES;
+  const char* kb = static_cast<const char*>(p.k) + (b * p.ks[0] + (h0 + hl) * E + sl * DPL) * S::ES;
+  const char* vb = static_cast<const char*>(p.v) + (b * p.vs[0] + (h0 + hl) * E + sl * DPL) * S::ES;
+  const u32x4 q = *reinterpret_cast<const u32x4*>(qb);
+  RowAcc<DPL> st;
+  st.m = -INFINITY;
+  st.l = 0.f;
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) st.acc[d] = 0.f;
+
+  auto load = [&](int64_t c, u32x4 (&kk)[NSTEP], u32x4 (&vv)[NSTEP]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s2 = 0; s2 < NSTEP; ++s2) {
+      const int64_t j = c * NSTEP + s2;
+      kk[s2] = u32x4{0u, 0u, 0u, 0u};
+      vv[s2] = u32x4{0u, 0u, 0u, 0u};
+      if (j < S_) {
+        kk[s2] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kb + j * p.ks[1] * S::ES));
+        vv[s2] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vb + j * p.vs[1] * S::ES));
+      }
+    }
+  };
+  auto fold = [&](int64_t c, const u32x4 (&kk)[NSTEP], const u32x4 (&vv)[NSTEP]) __attribute__((always_inline)) {
+    float lg[NSTEP];
+    float mx = st.m;
+#pragma unroll
+    for (int s2 = 0; s2 < NSTEP; ++s2) {
+      const float d = group_sum<G>(slice_dot<BF>(kk[s2], q));
+      lg[s2] = c * NSTEP + s2 < S_ ? d * p.c : -INFINITY;
+      mx = fmaxf(mx, lg[s2]);
+    }
+    if (mx == -INFINITY) return;
+    if (mx > st.m) {
+      const float alpha = __builtin_amdgcn_exp2f(st.m - mx);  // 0 while m is -inf
+      st.l *= alpha;
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) st.acc[d] *= alpha;
+      st.m = mx;
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < NSTEP; ++s2) {
+      const float e = __builtin_amdgcn_exp2f(lg[s2] - mx);
+      st.l += e;
+      const float pe = BF ? __uint_as_float(pack_bf16x2(e, 0.f) << 16) : e;
+      slice_pv<BF>(st.acc, pe, vv[s2]);
+    }
+  };
+
+  const int64_t stride = (int64_t)W * splits;
+  int64_t c = sp * W + wv;
+  if (c < nch) {
+    u32x4 kr[NBUF][NSTEP], vr[NBUF][NSTEP];
+#pragma unroll
+    for (int i = 0; i + 1 < NBUF; ++i)
+      if (c + i * stride < nch) load(c + i * stride, kr[i], vr[i]);
+    bool more = true;
+    while (more) {
+#pragma unroll
+      for (int i = 0; i < NBUF; ++i) {
+        if (more) {
+          const int64_t cp = c + (NBUF - 1) * stride;
+          if (cp < nch) load(cp, kr[(i + NBUF - 1) % NBUF], vr[(i + NBUF - 1) % NBUF]);
+          fold(c, kr[i], vr[i]);
+          c += stride;
+          more = c < nch;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) part[wv][hl][sl * DPL + d] = st.acc[d];
+  if (sl == 0) {
+    part[wv][hl][E] = st.m;
+    part[wv][hl][E + 1] = st.l;
+  }
+  __syncthreads();
+
+  // Merge the waves: wave w takes heads w, w + W, ... of the group.
+  constexpr int DPC = E >= 64 ? E / 64 : 1;
+  constexpr int ACTIVE = E / DPC;
+  for (int hh = wv; hh < HP; hh += W) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) mx = fmaxf(mx, part[w][hh][E]);
+    float l = 0.f, acc[DPC];
+#pragma unroll
+    for (int d = 0; d < DPC; ++d) acc[d] = 0.f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float wgt = __builtin_amdgcn_exp2f(part[w][hh][E] - mx);  // 0 for a wave that saw nothing
+        l = fmaf(wgt, part[w][hh][E + 1], l);
+        if (lane < ACTIVE) {
+#pragma unroll
+          for (int d = 0; d < DPC; ++d) acc[d] = fmaf(wgt, part[w][hh][lane * DPC + d], acc[d]);
+        }
+      }
+    }
+    const int64_t row = b * p.heads + h0 + hh;  // seq_q == 1
+    if (splits == 1) {
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      if (lane < ACTIVE) {
+        const int64_t oidx = row * E + lane * DPC;
+        if constexpr (BF) {
+          uint16_t* o = static_cast<uint16_t*>(p.out) + oidx;
+#pragma unroll
+          for (int d = 0; d < DPC; ++d) o[d] = (uint16_t)pack_bf16x2(acc[d] * inv, 0.f);
+        } else {
+          float* o = static_cast<float*>(p.out) + oidx;
+#pragma unroll
+          for (int d = 0; d < DPC; ++d) o[d] = acc[d] * inv;
+        }
+      }
+    } else {
+      const int64_t slot = row * splits + sp;
+      if (lane < ACTIVE) {
+#pragma unroll
+        for (int d = 0; d < DPC; ++d) p.part_acc[slot * E + lane * DPC + d] = acc[d];
+      }
+      if (lane == 0) {
+        p.part_ml[2 * slot] = mx;
+        p.part_ml[2 * slot + 1] = l;
+      }
+    }
+  }
+}
+
 // One wave per (batch, head, query) row: merges the row's partials of all splits.
+// The maxima come in one round (a lane per split); the P.V partials C at a time,
+// every load of a round issued before any is used (the kernel is latency-bound).
 template <int E, bool BF>
 __global__ __launch_bounds__(256) void flash_rows_combine_kernel(FlashParams p, int splits) {
   constexpr int DPC = E >= 64 ? E / 64 : 1;
   constexpr int ACTIVE = E / DPC;
+  constexpr int C = 8;
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= p.batch * p.heads * p.seq_q) return;
   const int64_t bh = row / p.seq_q, i = row - bh * p.seq_q;
   const int64_t b = bh / p.heads, h = bh - b * p.heads;
@@ -343,13 +537,24 @@ __global__ __launch_bounds__(256) void flash_rows_combine_kernel(FlashParams p, 
   float inv = 0.f;
   if (mx != -INFINITY) {
     float l = 0.f;
-    const float* pa = p.part_acc + row * splits * E + lane * DPC;
-    for (int t = 0; t < splits; ++t) {
-      const float wgt = __builtin_amdgcn_exp2f(ml[2 * t] - mx);
-      l = fmaf(wgt, ml[2 * t + 1], l);
-      if (lane < ACTIVE) {
+    const bool dims = lane < ACTIVE;
+    const float* pa = p.part_acc + row * splits * E + (dims ? lane * DPC : 0);
+    for (int t0 = 0; t0 < splits; t0 += C) {
+      float mt[C], lt[C], at[C][DPC];
 #pragma unroll
-        for (int d = 0; d < DPC; ++d) acc[d] = fmaf(wgt, pa[t * E + d], acc[d]);
+      for (int c = 0; c < C; ++c) {
+        const bool in = t0 + c < splits;
+        mt[c] = in ? ml[2 * (t0 + c)] : -INFINITY;
+        lt[c] = in ? ml[2 * (t0 + c) + 1] : 0.f;
+#pragma unroll
+        for (int d = 0; d < DPC; ++d) at[c][d] = in && dims ? pa[(int64_t)(t0 + c) * E + d] : 0.f;
+      }
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const float wgt = __builtin_amdgcn_exp2f(mt[c] - mx);
+        l = fmaf(wgt, lt[c], l);
+#pragma unroll
+        for (int d = 0; d < DPC; ++d) acc[d] = fmaf(wgt, at[c][d], acc[d]);
       }
     }
     inv = l > 0.f ? 1.f / l : 0.f;
@@ -380,16 +585,28 @@ __host__ __device__ inline int64_t rows_splits(int64_t batch, int64_t seq_q, int
   return s < 1 ? 1 : s;
 }
 
+// Splits of the call's route (the strides choose between the two kernels).
+static int64_t rows_call_splits(const FlashParams& p, int E, bool bf16) {
+  return rows_heads_route(p, E, bf16) ? rows_heads_splits(p.batch, p.seq_k, p.heads, E, bf16)
+                                      : rows_splits(p.batch, p.seq_q, p.seq_k, p.heads, E, bf16);
+}
+
+// The workspace a call of these shapes may need: its strides are not known
+// here, so the larger of the two routes' partials.
 int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, int E,
                                    bool bf16) {
   if (!rows_route(seq_q, bf16)) return 0;
-  const int64_t splits = rows_splits(batch, seq_q, seq_k, heads, E, bf16);
+  int64_t splits = rows_splits(batch, seq_q, seq_k, heads, E, bf16);
+  if (rows_heads_shapes(seq_q, seq_k, heads, E, bf16)) {
+    const int64_t hs = rows_heads_splits(batch, seq_k, heads, E, bf16);
+    splits = splits > hs ? splits : hs;
+  }
   if (splits <= 1) return 0;
   return batch * heads * seq_q * splits * (E + 2) * 4;
 }
 
 void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int E, bool bf16) {
-  const int64_t splits = rows_splits(p.batch, p.seq_q, p.seq_k, p.heads, E, bf16);
+  const int64_t splits = rows_call_splits(p, E, bf16);
   p.part_acc = static_cast<float*>(ws);
   p.part_ml = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.batch * p.heads * p.seq_q * splits * E * 4)
                  : nullptr;
@@ -399,10 +616,14 @@ void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int E, bool b
 template <int E, bool BF>
 static int rows_launch_t(const FlashParams& p, hipStream_t stream) {
   const int R = rows_per_wave(p.seq_q);
-  const int64_t gx = p.batch * p.heads * cdiv(p.seq_q, R);
-  const int64_t splits = rows_splits(p.batch, p.seq_q, p.seq_k, p.heads, E, BF);
+  const bool heads = rows_heads_route(p, E, BF);
+  const int64_t gx = heads ? p.batch * (p.heads / HeadsShape<E, BF>::HP) : p.batch * p.heads * cdiv(p.seq_q, R);
+  const int64_t splits = rows_call_splits(p, E, BF);
   if (gx > 0x7fffffff) return CA_DECLINED;
-  if (R == 1)
+  if (heads)
+    hipLaunchKernelGGL((flash_rows_heads_kernel<E, BF>), dim3((unsigned)gx, (unsigned)splits), dim3(64 * kRowsWaves),
+                       0, stream, p);
+  else if (R == 1)
     hipLaunchKernelGGL((flash_rows_kernel<E, BF, 1>), dim3((unsigned)gx, (unsigned)splits), dim3(64 * kRowsWaves),
                        0, stream, p);
   else
@@ -417,7 +638,8 @@ static int rows_launch_t(const FlashParams& p, hipStream_t stream) {
 }
 
 int flash_rows_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
-  const int64_t need = flash_rows_workspace_bytes(p.batch, p.seq_q, p.seq_k, p.heads, E, bf16 != 0);
+  const int64_t splits = rows_call_splits(p, E, bf16 != 0);
+  const int64_t need = splits > 1 ? p.batch * p.heads * p.seq_q * splits * (E + 2) * 4 : 0;
   if (need > 0 && (p.part_acc == nullptr || p.workspace_bytes < need)) return CA_DECLINED;
   if (bf16) {
     switch (E) {

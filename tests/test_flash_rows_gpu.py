@@ -65,6 +65,46 @@ def test_strided_views(cuda, dtype):
     assert_close(out, attention(values(q), values(k), values(v), d ** -0.5), dtype, paged=False)
 
 
+def heads_per_load(d, dtype):
+    """Heads one wave load instruction covers on the single-row route for packed
+    heads (64 lanes of 16 bytes over rows of d elements; csrc/ca_rows.hip)."""
+    return 64 // (d * dtype.itemsize // 16)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("sk", [1, 5, 64, 300, 1024, 1025, 2049])
+def test_single_row_packed_heads(cuda, dtype, d, sk):
+    """One query row with the heads side by side (head stride d) and a head count
+    that is a multiple of the heads per load: up to 1024 keys the route that reads
+    each key's heads as one run, with the keys split over blocks and merged by the
+    combine kernel, past that the per-head route; also with k/v as chunks of a
+    fused projection (still packed heads)."""
+    h = 2 * heads_per_load(d, dtype)
+    run(3, 1, sk, h, d, dtype, False, seed=sk + d, device=cuda)
+    g = torch.Generator().manual_seed(sk)
+    kv = torch.randn(2, sk, 2 * h * d, generator=g).to(dtype).to(cuda)
+    k, v = (kv[..., i * h * d:(i + 1) * h * d].view(2, sk, h, d) for i in (0, 1))
+    q = torch.randn(2, 1, h, d, generator=g).to(dtype).to(cuda)
+    out = flash_attn_func(q, k, v, causal=True)
+    assert_close(out, attention(values(q), values(k), values(v), d ** -0.5, True), dtype, paged=False)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_single_row_unpacked_heads(cuda, dtype):
+    """One query row whose k/v heads are not side by side (head stride 2d, a
+    strided view) takes the per-head route and agrees as well."""
+    d, sk = 64, 1000
+    h = heads_per_load(d, dtype)
+    g = torch.Generator().manual_seed(4)
+    kv = torch.randn(2, sk, h, 2 * d, generator=g).to(dtype).to(cuda)
+    k, v = kv[..., :d], kv[..., d:]
+    assert k.stride(2) == 2 * d
+    q = torch.randn(2, 1, h, d, generator=g).to(dtype).to(cuda)
+    out = flash_attn_func(q, k, v)
+    assert_close(out, attention(values(q), values(k), values(v), d ** -0.5), dtype, paged=False)
+
+
 def test_scale_and_large_logits(cuda):
     """A large scale (logits spread over many chunks' maxima) in fp32."""
     run(2, 4, 2000, 2, 128, torch.float32, False, seed=9, device=cuda, scale=0.5)
