@@ -151,6 +151,11 @@ def _stride(t, i):
     return 0 if t.shape[i] == 1 else t.stride(i)
 
 
+def _strides3(st, sh):
+    """The first three of ``st`` (a tensor's strides), 0 where ``sh`` has size 1."""
+    return (0 if sh[0] == 1 else st[0], 0 if sh[1] == 1 else st[1], 0 if sh[2] == 1 else st[2])
+
+
 def _rows_ok(t, hd):
     """Heads and dims contiguous (any token stride: chunks of a fused projection)."""
     return t.stride(-1) == 1 and (t.shape[-2] == 1 or t.stride(-2) == hd)
@@ -255,13 +260,15 @@ class Module:
         dim]`` when n > 1, appended at ``lens``)."""
         if not (_plain(q) and _plain(page_table) and isinstance(lens, torch.Tensor)):
             return None
-        nd = q.dim()
-        if nd not in (3, 4) or (nd == 4 and q.shape[1] != 1):
+        qsh = q.shape
+        nd = len(qsh)
+        if nd not in (3, 4) or (nd == 4 and qsh[1] != 1):
             return None
-        b, heads, hd = q.shape[0], q.shape[-2], q.shape[-1]
-        if q.dtype not in DTYPES or hd not in HEAD_DIMS or not _rows_ok(q, hd):
+        b, heads, hd = qsh[0], qsh[-2], qsh[-1]
+        dt = q.dtype
+        if dt not in DTYPES or hd not in HEAD_DIMS or not _rows_ok(q, hd):
             return None
-        if not _caches_ok(k_cache, v_cache, q.dtype, heads, hd):
+        if not _caches_ok(k_cache, v_cache, dt, heads, hd):
             return None
         page = k_cache.shape[2]
         if page_table.dim() != 2 or page_table.dtype != torch.int32 or page_table.shape[0] != b \
@@ -290,9 +297,10 @@ class Module:
             return None
         q_stride = _stride(q, 0)
         kv_stride = _stride(k, 0) if store else 0
-        if not (aligned(q, (q_stride,)) and aligned(k_cache) and aligned(v_cache)):
-            return None
-        if store and not (aligned(k, (kv_stride,)) and aligned(v, (kv_stride,))):
+        # 16-byte vectors: pointers and element strides (a multiple of 16 / esize)
+        qp, kcp, vcp = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr()
+        knp, vnp = (k.data_ptr(), v.data_ptr()) if store else (0, 0)
+        if (qp | kcp | vcp | knp | vnp) % 16 or (q_stride | kv_stride) % (16 // _ESIZE[dt]):
             return None
         nblocks = k_cache.shape[0]
         # The data-dependent rules (_C.mojo:139-153), on the host.
@@ -305,22 +313,18 @@ class Module:
         page_table = _index_on(page_table, dev)
         if slots is not None:
             slots = _index_on(slots, dev)
-        out = dst if dst is not None else torch.empty(q.shape, dtype=q.dtype, device=dev)
+        out = dst if dst is not None else torch.empty(qsh, dtype=dt, device=dev)
         key = (b, heads, hd, page, width)
         ws_bytes = self._dec_ws.get(key)
         if ws_bytes is None:
             ws_bytes = self._dec_ws[key] = self.lib.ca_decode_workspace_bytes(*key)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-        args = DecodeArgs(
-            q=q.data_ptr(), q_stride=q_stride, k_cache=k_cache.data_ptr(),
-            v_cache=v_cache.data_ptr(), k_new=k.data_ptr() if store else None,
-            v_new=v.data_ptr() if store else None, kv_stride=kv_stride,
-            slots=slots.data_ptr() if slots is not None else None, lens=lens.data_ptr(),
-            page_table=page_table.data_ptr(), page_table_width=width, out=out.data_ptr(),
-            num_seqs=b, num_heads=heads, head_dim=hd, page_size=page, num_blocks=nblocks,
-            scale=float(hd) ** -0.5 if scale is None else float(scale), dtype=DTYPES[q.dtype],
-            workspace=ws.data_ptr() if ws is not None else None, workspace_bytes=ws_bytes,
-            new_tokens=n if store else 0)
+        wst = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None  # held past the launch
+        ws = wst.data_ptr() if ws_bytes else None
+        args = DecodeArgs(qp, q_stride, kcp, vcp, knp or None, vnp or None, kv_stride,
+                          slots.data_ptr() if slots is not None else None, lens.data_ptr(),
+                          page_table.data_ptr(), width, out.data_ptr(), b, heads, hd, page, nblocks,
+                          float(hd) ** -0.5 if scale is None else float(scale), DTYPES[dt],
+                          ws, ws_bytes, n if store else 0)
         rc = self.lib.ca_decode(ctypes.byref(args), _stream(dev))
         if rc == CA_DECLINED:
             return None
@@ -387,42 +391,45 @@ class Module:
     def flash(self, rt, q, k, v, scale, causal, ws, ws_bytes):
         """flash_attn_func over q/k/v ``[batch, seq, heads, dim]`` (MHA, dims
         contiguous). Returns the output, the workspace bytes it needs when
-        ``ws_bytes`` is short (an int), or None (_C.mojo:232-316)."""
-        if not all(isinstance(x, torch.Tensor) and _plain(x) for x in (q, k, v)):
+        ``ws_bytes`` is short (an int), or None (_C.mojo:232-316).  Small calls
+        are bound by this host work, so each tensor's shape and strides are read
+        once."""
+        if not (type(q) in _PLAIN and type(k) in _PLAIN and type(v) in _PLAIN):
             return None
-        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        qsh, ksh = q.shape, k.shape
+        if len(qsh) != 4 or len(ksh) != 4 or v.shape != ksh:
             return None
-        b, sq, heads, hd = q.shape
-        sk = k.shape[1]
-        if q.dtype not in DTYPES or hd not in HEAD_DIMS or sq < 1 or sk < 1:
+        b, sq, heads, hd = qsh
+        sk = ksh[1]
+        dt = q.dtype
+        if dt not in DTYPES or hd not in HEAD_DIMS or sq < 1 or sk < 1:
             return None
-        if k.shape[0] != b or k.shape[2] != heads or k.shape[3] != hd or k.dtype != q.dtype \
-                or v.dtype != q.dtype:
+        if ksh[0] != b or ksh[2] != heads or ksh[3] != hd or k.dtype != dt or v.dtype != dt:
             return None
-        if v.shape != k.shape:
-            return None
-        if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1:
+        qst, kst, vst = q.stride(), k.stride(), v.stride()
+        if qst[3] != 1 or kst[3] != 1 or vst[3] != 1:
             return None
         if not (causal is True or causal is False):
             return None
         dev = q.device
-        if not q.is_cuda or not _on_gpu(dev, k, v):
+        if not q.is_cuda or k.device != dev or v.device != dev:
             return None
-        qs, ks, vs = ([_stride(x, i) for i in range(3)] for x in (q, k, v))
-        if not (aligned(q, qs) and aligned(k, ks) and aligned(v, vs)):
+        qs, ks, vs = _strides3(qst, qsh), _strides3(kst, ksh), _strides3(vst, ksh)
+        # 16-byte vectors: pointers and element strides (a multiple of 16 / esize)
+        qp, kp, vp = q.data_ptr(), k.data_ptr(), v.data_ptr()
+        unit = 16 // _ESIZE[dt]
+        if (qp | kp | vp) % 16 or (qs[0] | qs[1] | qs[2] | ks[0] | ks[1] | ks[2] | vs[0] | vs[1] | vs[2]) % unit:
             return None
-        need = self.flash_workspace_bytes(q, k)
+        key = (b, sq, sk, heads, hd, dt)
+        need = self._flash_ws.get(key)
+        if need is None:
+            need = self._flash_ws[key] = self._flash_ws_query(q, k)
         if need > ws_bytes:
             return int(need)
-        out = torch.empty((b, sq, heads, hd), dtype=q.dtype, device=dev)
-        args = FlashArgs(
-            q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), out=out.data_ptr(), batch=b,
-            seq_q=sq, seq_k=sk, num_heads=heads, head_dim=hd,
-            q_strides=(ctypes.c_int64 * 3)(*qs), k_strides=(ctypes.c_int64 * 3)(*ks),
-            v_strides=(ctypes.c_int64 * 3)(*vs),
-            scale=float(hd) ** -0.5 if scale is None else float(scale),
-            causal=1 if causal else 0, dtype=DTYPES[q.dtype], workspace=ws or None,
-            workspace_bytes=ws_bytes)
+        out = torch.empty(qsh, dtype=dt, device=dev)
+        args = FlashArgs(qp, kp, vp, out.data_ptr(), b, sq, sk, heads, hd, qs, ks, vs,
+                         float(hd) ** -0.5 if scale is None else float(scale), 1 if causal else 0,
+                         DTYPES[dt], 0, ws or None, ws_bytes)
         rc = self.lib.ca_flash(ctypes.byref(args), _stream(dev))
         if rc == CA_DECLINED:
             return None
