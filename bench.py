@@ -22,7 +22,8 @@ state whatever W the caller passes.
 The JSON line also carries:
 
 * ``roofline`` for the decode kernel: algorithmic bytes per call / the event-timed
-  average call duration against MI355X's 8 TB/s;
+  average call duration against MI355X's 8 TB/s (``frac_cold`` and
+  ``us_per_call_cold``: the same with the caches flushed before each call);
 * ``prefill``: BASELINE cfg4 (bf16 causal N=4 L=S=4096 H=32 E=128, q/k/v
   strided chunks of a fused projection) in TFLOP/s against the 2.5 PFLOP/s dense
   bf16 MFMA peak, with its own roofline object;
@@ -594,6 +595,10 @@ def main():
     wall, ms, nramp = timed(step, args.steps, args.warmup)
     call_ms = float(np.mean(ms))
     gbs_kernel = w["bytes"] / (call_ms * 1e-3) / 1e9
+    # cold: caches flushed before each sample (the 1 GiB fill leaves the caches
+    # full of dirty lines, whose write-back the call then pays for)
+    flush = Flush(dev)
+    cmed, cmin, cmax = cold(step, flush, 15)
     value = w["bytes"] * args.steps / wall / 1e9
     res = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
@@ -606,8 +611,11 @@ def main():
         "clock_ramp_ms": RAMP_S * 1e3, "clock_ramp_calls": nramp,
         "us_per_call": round(call_ms * 1e3, 2),
         "us_per_call_median": round(float(np.median(ms)) * 1e3, 2),
+        "us_per_call_cold": round(cmed * 1e3, 2), "us_per_call_cold_min_max": [round(cmin * 1e3, 2),
+                                                                               round(cmax * 1e3, 2)],
         "roofline": {"bound": "hbm", "achieved": round(gbs_kernel, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs_kernel / HBM_PEAK_GBS, 4),
+                     "frac_cold": round(w["bytes"] / (cmed * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "traffic": traffic_bytes("decode"),
                      "kernel": "decode_tiles_kernel<128,bf16,64-key tiles> + decode_tiles_combine_kernel "
                                "(the call's two dispatches, timed together)",
@@ -629,6 +637,7 @@ def main():
         pwall, pms, pramp = timed(pstep, psteps, pwarm)
         flop = causal_flop(N, H, E, L, L)
         pcall = float(np.mean(pms))
+        pcmed, pcmin, pcmax = cold(pstep, flush, 10)
         tf = flop / (pcall * 1e-3) / 1e12
         res["prefill"] = {
             "workload": "flash_attn_func bf16 causal N=4 L=S=4096 H=32 E=128, q/k/v strided "
@@ -636,8 +645,11 @@ def main():
             "value": round(flop * len(pms) / pwall / 1e12, 2), "unit": "TFLOP/s",
             "steps": psteps, "warmup": pwarm, "clock_ramp_ms": RAMP_S * 1e3, "clock_ramp_calls": pramp,
             "us_per_call": round(pcall * 1e3, 1), "us_per_call_median": round(float(np.median(pms)) * 1e3, 1),
+            "us_per_call_cold": round(pcmed * 1e3, 1),
+            "us_per_call_cold_min_max": [round(pcmin * 1e3, 1), round(pcmax * 1e3, 1)],
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                         "frac_cold": round(flop / (pcmed * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
                          "traffic": traffic_bytes("prefill"), "kernel": "flash_bf16_p64_kernel<128>",
                          "algorithmic_flop": flop},
         }

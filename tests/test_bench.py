@@ -56,6 +56,7 @@ def test_json_line_carries_the_contract(cuda):
         assert 0 < roof["frac"] < 1 and roof["traffic"] > 0
         assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
     assert d["roofline"]["bound"] == "hbm" and d["prefill"]["roofline"]["bound"] == "mfma"
+    assert d["us_per_call_cold"] > 0 and d["prefill"]["us_per_call_cold"] > 0
     # the clock ramp runs before the W warm-up calls of each leg, and is reported
     assert d["clock_ramp_calls"] > 0 and d["prefill"]["clock_ramp_calls"] > 0
     # every other BASELINE config, with its work, timings and roofline fraction
