@@ -338,7 +338,7 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
   // g + G*j, so one wave instruction reads G consecutive rows of one unit (the unit
   // is the same for every lane, since G divides 16) and a batch spans all 4 units.
   constexpr bool BY_UNIT = NU >= G;
-  constexpr int UPG = BY_UNIT ? NU / G : 1;  // units per group (256-key tiles)
+  constexpr int UPG = BY_UNIT ? NU / G : 1;  // units per group (BY_UNIT)
   constexpr int NV = BY_UNIT ? UPG : NU;     // unit bases a lane holds
   constexpr int R = TK / G;                  // rows per lane
   constexpr int B = R < 16 ? R : 16;         // loads in flight

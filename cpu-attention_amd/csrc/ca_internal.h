@@ -41,7 +41,7 @@ struct DecodeParams {
   // The one-token append done inside the decode (nullptr: none): token s of
   // k_new/v_new ([N, H, W] word rows, sequence stride kv_stride_w) is written to
   // the cache at position lens[s] by the wave whose tile holds that position,
-  // before that wave reads the tile.
+  // which also attends it.
   const uint32_t* k_new;
   const uint32_t* v_new;
   int64_t kv_stride_w;
