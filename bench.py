@@ -38,7 +38,8 @@ The JSON line also carries:
   reference cannot be built here) on the box's physical host cores, over the whole
   cfg3 batch for CPU_BUDGET_S seconds (and the prefill port on one (batch, head) of
   cfg4 for as long), labelled as a substitute, with the reference's own published
-  CPU figures beside it.
+  CPU figures beside it and, for the prefill, torch's CPU SDPA on the same cores
+  (``prefill.cpu_baseline.torch_sdpa``) as a second substitute.
 
 ``roofline.traffic`` is the HBM bytes one call moves, from rocprofv3 --pmc runs of
 ``python bench.py --profile-pass`` (one 1 GiB device copy, then a few calls of
@@ -488,7 +489,34 @@ def cpu_prefill_baseline(budget_s=CPU_BUDGET_S):
                     "rate, so read the published figure as the CPU baseline",
             "sample": f"C port of the reference's prefill, one (batch, head) of the config "
                       f"(L=S=4096 E=128 causal bf16), {reps} calls in {reps * dt:.1f} s, {dt * 1e3:.1f} ms/call",
-            "published": PUBLISHED["prefill"]}
+            "published": PUBLISHED["prefill"], "torch_sdpa": cpu_sdpa_baseline(threads, budget_s / 2)}
+
+
+def cpu_sdpa_baseline(threads, budget_s):
+    """torch's CPU scaled_dot_product_attention on the same prefill shape (8 of its
+    heads per call, bf16, causal), on the host's physical cores: a second
+    substitute for the reference's CPU path, not the reference."""
+    old = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        h, L, e = 8, 4096, 128
+        g = torch.Generator().manual_seed(2)
+        q, k, v = (torch.randn(1, h, L, e, generator=g).bfloat16() for _ in range(3))
+        sdpa = torch.nn.functional.scaled_dot_product_attention
+        sdpa(q, k, v, is_causal=True)  # warm
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            sdpa(q, k, v, is_causal=True)
+            reps += 1
+            if time.perf_counter() - t0 >= budget_s and reps >= 3:
+                break
+        dt = (time.perf_counter() - t0) / reps
+    finally:
+        torch.set_num_threads(old)
+    flop = 4 * h * e * L * (L + 1) / 2
+    return {"value": round(flop / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "torch",
+            "sample": f"torch {torch.__version__} CPU SDPA, bf16 causal [1, 8 heads, 4096, 128], {reps} calls "
+                      f"in {reps * dt:.1f} s, {dt * 1e3:.1f} ms/call"}
 
 
 # ---------------------------------------------------------------------------

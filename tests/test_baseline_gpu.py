@@ -1,7 +1,7 @@
 """The BASELINE decode workloads at full size on the GPU: cfg3 with every sequence
 checked against the float64 oracle, cfg2 with every row, and cfg5's store + decode
 loop with the cache bytes compared to the layout oracle after staging and after the
-first and last steps."""
+first and last steps (the pages each step appends to after every step)."""
 
 import numpy as np
 import pytest
@@ -87,7 +87,8 @@ def test_cfg5_store_and_decode_loop(cuda):
     """N=128 H=32 E=128 page=16 bf16: stage prompts of lengths U[64,1024] through
     reshape_and_cache with ~10% negative (padding) slots, then 32 decode steps each
     appending one token and attending.  Cache bytes equal the layout oracle after
-    staging and after every step; sampled rows match the float64 oracle."""
+    staging, the pages each step appends to after every step, and the whole caches
+    after the first and last steps; sampled rows match the float64 oracle."""
     n, h, e, page, steps = 128, 32, 128, 16, 32
     rng = np.random.default_rng(5)
     lens = rng.integers(64, 1025, size=n)
@@ -127,6 +128,11 @@ def test_cfg5_store_and_decode_loop(cuda):
         s_np = layout.append_slots(cur.cpu().numpy(), table.numpy(), page)
         layout.store(kw, vw, row_words(kn[:, 0]), row_words(vn[:, 0]), s_np, page)
         cur = cur + 1
+        # every step: the pages the step appended to, byte for byte
+        blocks = np.unique(s_np[s_np >= 0] // page)
+        bsel = torch.from_numpy(blocks).to(cuda)
+        np.testing.assert_array_equal(cache_words(kc[bsel]), kw[blocks])
+        np.testing.assert_array_equal(cache_words(vc[bsel]), vw[blocks])
         if step in (0, steps - 1):
             np.testing.assert_array_equal(cache_words(kc), kw)
             np.testing.assert_array_equal(cache_words(vc), vw)
