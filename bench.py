@@ -593,7 +593,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the ops run within one device and this build "
-              "has no multi-GPU path (see DESIGN.md for how it would shard). Use --gpus 1.",
+              "has no multi-GPU path (sequences or heads would shard across GPUs with no "
+              "cross-GPU traffic inside a call). Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
