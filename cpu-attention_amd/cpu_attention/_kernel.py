@@ -12,11 +12,18 @@ of ducviet00/cpu-attention) whose entries ``decode``, ``store`` and ``flash``
 (_mojo/src/_C.mojo:87-316) read torch tensors in place, validate them, and return
 ``None`` for anything they do not take.  This build keeps that module surface --
 ``module().decode/.store/.flash`` with the same positional arguments and the same
-``None`` / ``int`` return conventions -- but the entries are thin Python shims:
-they read tensor metadata through torch's public API, apply the same acceptance
-rules, allocate outputs with ``torch.empty`` on the tensors' GPU, and call the
-C ABI of ``libcpu_attention_hip.so`` (include/cpu_attention_hip.h) through
-ctypes on torch's current HIP stream.  The kernels run asynchronously.
+``None`` / ``int`` return conventions.  The entries read tensor metadata in
+place, apply the same acceptance rules, allocate outputs from torch's caching
+allocator on the tensors' GPU, and call the C ABI of ``libcpu_attention_hip.so``
+(include/cpu_attention_hip.h) on torch's current HIP stream; the kernels run
+asynchronously.  Two bindings implement them with the same rules and results:
+
+- ``NativeModule`` (the default when ``_binding`` is built): the argument
+  handling in a small C++ extension (csrc/ca_binding.cpp), as the reference's
+  own native module does it; a few microseconds per call;
+- ``Module``: the same in Python over ctypes, which is also the binding a
+  maintainer of the reference would add on its side.  It serves when the
+  extension is not built, or when ``CPU_ATTENTION_BINDING=ctypes``.
 
 Data-dependent rules (a slot past the cache's end, a length beyond the page
 table's capacity) need the index values.  By default they are checked on the
@@ -26,7 +33,8 @@ synchronisation when they live on the GPU).  ``set_host_checks(False)`` (or
 out of bounds either way (such tokens are not stored, such positions not read),
 but no ValueError is raised.
 
-Environment: ``CPU_ATTENTION_LIB`` names another build of the library.
+Environment: ``CPU_ATTENTION_LIB`` names another build of the library;
+``CPU_ATTENTION_BINDING=ctypes`` selects the ctypes binding.
 """
 
 import ctypes
@@ -100,6 +108,8 @@ def set_host_checks(enabled):
     previous setting."""
     old = _HOST_CHECKS[0]
     _HOST_CHECKS[0] = bool(enabled)
+    if _MODULE is not None and isinstance(_MODULE, NativeModule):
+        _MODULE.binding.set_host_checks(_HOST_CHECKS[0])
     return old
 
 
@@ -438,6 +448,46 @@ class Module:
         return out
 
 
+def _stream_of_index(index):
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+class NativeModule(Module):
+    """``Module`` with decode/store/flash's argument handling in the native
+    extension ``_binding`` (csrc/ca_binding.cpp): the same rules in the same
+    order, the same results.  The entries are the extension's functions
+    themselves, so a call runs no Python code of this package."""
+
+    ENTRIES = ("ca_decode", "ca_store", "ca_flash", "ca_decode_workspace_bytes",
+               "ca_flash_workspace_bytes", "ca_status_string")
+
+    def __init__(self, lib, binding):
+        super().__init__(lib)
+        addrs = tuple(ctypes.cast(getattr(lib, name), ctypes.c_void_p).value for name in self.ENTRIES)
+        binding.init(addrs, _PLAIN, _RAW_STREAM or _stream_of_index, _HOST_CHECKS[0])
+        self.binding = binding
+        self.decode = binding.decode
+        self.store = binding.store
+        self.flash = binding.flash
+
+    def _decode(self, q, k_cache, v_cache, k, v, slots, lens, page_table, scale, dst, n):
+        return self.binding.decode(None, q, k_cache, v_cache, k, v, slots, lens, page_table, scale, dst, n)
+
+
+def _native_binding():
+    """The ``_binding`` extension, or None when it is not built or
+    ``CPU_ATTENTION_BINDING=ctypes``.  A built extension that fails to load
+    raises."""
+    if os.environ.get("CPU_ATTENTION_BINDING", "native") == "ctypes":
+        return None
+    import importlib
+    import importlib.util
+
+    if importlib.util.find_spec(__package__ + "._binding") is None:
+        return None
+    return importlib.import_module(__package__ + "._binding")
+
+
 _MODULE = None
 _LOCK = threading.Lock()
 
@@ -452,8 +502,16 @@ def module():
                 if not os.path.exists(path):
                     raise RuntimeError("cpu_attention: the gfx950 kernel library is not built; run "
                                        "`python cpu-attention_amd/build.py`")
-                _MODULE = Module(load_library(path))
+                lib = load_library(path)
+                binding = _native_binding()
+                _MODULE = NativeModule(lib, binding) if binding is not None else Module(lib)
     return _MODULE
+
+
+def ctypes_module():
+    """A ``Module`` (the ctypes binding) over the loaded library, whichever
+    binding ``module()`` uses."""
+    return Module(module().lib)
 
 
 def runtime():

@@ -6,11 +6,16 @@ check fired (and not the GPU build's own device rule, which comes last), and a
 well-formed call with CPU tensors is refused with the device message.
 """
 
+import os
+import subprocess
+import sys
+
 import pytest
 import torch
 
 import cpu_attention as C
 from cpu_attention import _kernel as K
+from conftest import PKG
 
 
 def paged():
@@ -173,9 +178,11 @@ def test_cpu_tensors_meet_the_device_rule():
         C.reshape_and_cache(torch.randn(3, 4, 64), torch.randn(3, 4, 64), kc, vc, torch.arange(3))
 
 
-def test_native_entries_decline_with_none():
-    """The module entries keep the reference's None convention (_C.mojo:87-316)."""
-    mod, rt = K.module(), K.runtime()
+@pytest.mark.parametrize("binding", ["default", "ctypes"])
+def test_native_entries_decline_with_none(binding):
+    """The module entries keep the reference's None convention (_C.mojo:87-316),
+    through either binding."""
+    mod, rt = (K.module() if binding == "default" else K.ctypes_module()), K.runtime()
     q, kc, vc, bt = paged()
     lens = torch.full((2,), 4, dtype=torch.int32)
     assert mod.decode(rt, q, kc, vc, None, None, None, lens, bt, None, None) is None
@@ -185,6 +192,34 @@ def test_native_entries_decline_with_none():
     assert mod.flash(rt, x, x, x, None, 1, 0, 0) is None  # causal must be True/False
     assert mod.flash(rt, x, x, x, None, True, 0, 0) is None  # CPU tensors
     assert mod.tier() == "gfx950" and mod.amx_available() is False
+
+
+def test_native_binding_is_the_default_when_built():
+    """The C++ binding serves the entries once built; CPU_ATTENTION_BINDING=ctypes
+    selects the ctypes one (checked in a fresh interpreter)."""
+    import importlib.util
+    built = importlib.util.find_spec("cpu_attention._binding") is not None
+    assert isinstance(K.module(), K.NativeModule) == built
+    if built:
+        assert K.module().decode is K.module().binding.decode
+    code = ("import sys; sys.path.insert(0, %r); from cpu_attention import _kernel as K; "
+            "print(type(K.module()).__name__)" % PKG)
+    env = dict(os.environ, CPU_ATTENTION_BINDING="ctypes")
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, check=True)
+    assert out.stdout.strip() == "Module"
+
+
+def test_native_binding_argument_errors():
+    """Wrong argument counts and scales raise as the ctypes binding's would."""
+    mod = K.module()
+    if not isinstance(mod, K.NativeModule):
+        pytest.skip("native binding not built")
+    with pytest.raises(TypeError):
+        mod.decode(None, 1, 2)
+    with pytest.raises(TypeError):
+        mod.flash(None)
+    with pytest.raises(TypeError):
+        mod.store()
 
 
 def test_host_info():
