@@ -136,7 +136,8 @@ static int decode_entry(const ca_decode_args* a, void* stream, bool noalloc) {
   // into the decode kernel: the wave whose tile holds position lens[s] writes it
   // to the cache and attends it, so one launch does both.  Larger batches,
   // several tokens, or a store at given slots (which need not be the position
-  // the row attends) go through the store kernel first.
+  // the row attends) go through a store kernel first: the scatter kernel for one
+  // token per sequence (each on a page of its own), the staging one for a prompt.
   const bool fused = a->k_new && !a->slots && per_seq == 1 &&
                      a->num_seqs * a->num_heads <= kFusedAppendMaxRows;
   if (a->k_new && !fused) {
@@ -155,7 +156,7 @@ static int decode_entry(const ca_decode_args* a, void* stream, bool noalloc) {
     sp.heads = a->num_heads;
     sp.page = a->page_size;
     sp.nblocks = a->num_blocks;
-    const int r = store_launch(sp, (int)words, st);
+    const int r = per_seq == 1 ? store_scatter_launch(sp, (int)words, st) : store_launch(sp, (int)words, st);
     if (r != CA_OK) return r;
   }
 

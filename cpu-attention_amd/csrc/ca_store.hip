@@ -126,6 +126,58 @@ __global__ __launch_bounds__(256) void store_kernel(StoreParams p) {
   }
 }
 
+// One token per sequence (the decode-time append, and the engine path's store at
+// a slot): every token lands on a page of its own, so store_kernel's staging, which
+// merges consecutive slots of a page into 64-byte K word rows, has nothing to
+// merge, and its 16-token blocks leave most of the chip idle on a small batch.
+// Here one wave moves one (token, head): lane w moves K word w (one 4-byte store
+// per word row of the page) and lanes below W/4 move the V row in 16-byte pieces.
+// A block is 4 waves (4 heads of one token).
+template <int W>
+__global__ __launch_bounds__(256) void scatter_kernel(StoreParams p) {
+  constexpr int KPL = (W + kWave - 1) / kWave;  // K words per lane
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t hg = cdiv(p.heads, 4);
+  const int64_t i = blockIdx.x / hg;
+  const int64_t h = (blockIdx.x - i * hg) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (i >= p.ntok || h >= p.heads) return;
+  int64_t blk, off;
+  store_target(p, i, blk, off);
+  if (blk < 0) return;
+  const int64_t src = i * p.tok_stride_w + h * W;
+  const int64_t row0 = (blk * p.heads + h) * p.page;  // the (block, head)'s first row
+  uint32_t kw[KPL];
+  u32x4 vv = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int c = 0; c < KPL; ++c) {
+    const int w = lane + kWave * c;
+    kw[c] = w < W ? p.key[src + w] : 0u;
+  }
+  if (lane < W / 4) vv = *reinterpret_cast<const u32x4*>(p.value + src + 4 * lane);
+#pragma unroll
+  for (int c = 0; c < KPL; ++c) {
+    const int w = lane + kWave * c;
+    if (w < W) p.kc[row0 * W + (int64_t)w * p.page + off] = kw[c];
+  }
+  if (lane < W / 4) *reinterpret_cast<u32x4*>(p.vc + (row0 + off) * W + 4 * lane) = vv;
+}
+
+int store_scatter_launch(const StoreParams& sp, int W, hipStream_t stream) {
+  if (sp.ntok == 0) return CA_OK;
+  if (sp.per_seq != 1) return CA_DECLINED;
+  const int64_t nb = sp.ntok * cdiv(sp.heads, 4);
+  if (nb > 0x7fffffff) return CA_DECLINED;
+  dim3 grid((unsigned)nb), block(256);
+  switch (W) {
+    case 16: hipLaunchKernelGGL(scatter_kernel<16>, grid, block, 0, stream, sp); break;
+    case 32: hipLaunchKernelGGL(scatter_kernel<32>, grid, block, 0, stream, sp); break;
+    case 64: hipLaunchKernelGGL(scatter_kernel<64>, grid, block, 0, stream, sp); break;
+    case 128: hipLaunchKernelGGL(scatter_kernel<128>, grid, block, 0, stream, sp); break;
+    default: return CA_DECLINED;
+  }
+  return ca_launch_status();
+}
+
 int store_launch(const StoreParams& sp, int W, hipStream_t stream) {
   if (sp.ntok == 0) return CA_OK;
   const int64_t nb = cdiv(sp.ntok, kStoreTok) * cdiv(sp.heads, 256 / W);
