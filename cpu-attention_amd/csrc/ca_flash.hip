@@ -437,7 +437,11 @@ struct P64Rows {
   }
 
   // Q to the AGPRs, O = 0 (written by MFMAs, so the accumulators are born in
-  // AGPRs), and the softmax state reset.
+  // AGPRs; volatile, so each block gets its own MFMA rather than a copy of one
+  // block's zeros), and the softmax state reset.  settle() must follow.  The
+  // compiler may write the zero operand just before (it does not know the asm
+  // is an MFMA, which reads a VGPR that VALU code wrote only 2 wait states later),
+  // hence the s_nop.
   __device__ __forceinline__ void q_home() {
     const bf16x8 z = bf16x8{};
 #pragma unroll
@@ -445,7 +449,8 @@ struct P64Rows {
 #pragma unroll
       for (int s = 0; s < NS; ++s) asm("" : "+a"(qr[cb][s]));
 #pragma unroll
-      for (int d = 0; d < ND; ++d) asm("v_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(o[cb][d]) : "v"(z));
+      for (int d = 0; d < ND; ++d)
+        asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(o[cb][d]) : "v"(z));
       m[cb] = -INFINITY;
       nmu[cb] = 0.f;
       l[cb] = 0.f;
@@ -464,6 +469,18 @@ struct P64Rows {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // The wait states after MFMAs that wrote O, then the accumulators marked as
+  // redefined here.  The MFMAs are inline assembly, so the compiler does not know
+  // their results land late: a copy it makes of O on its own (to merge two
+  // control-flow paths, say) could otherwise read the registers too early.
+  __device__ __forceinline__ void settle() {
+    mfma_guard();
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int d = 0; d < ND; ++d) asm volatile("" : "+a"(o[cb][d]));
   }
 
   // Keys of tile t row (cb, li) may see: key 32kt + 8(r/4) + 4hf + r%4 of the
@@ -817,6 +834,7 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
       tv.issue(voff);
     }
     w.q_home();
+    w.settle();
     bool bad = false;
     if (nkt > 0) {
       loads_landed_barrier<2 * NL>();  // K(0) and K(1) have landed

@@ -193,3 +193,25 @@ def test_safe_pass_for_one_pass_of_a_causal_pair(cuda, d, bad_pass):
     out = flash_attn_func(q, k, v, causal=True)
     ref = attention(values(q), values(k), values(v), d ** -0.5, True)
     assert_close(out, ref, torch.bfloat16, paged=False)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal,sq", [(True, 1536), (False, 600)])
+def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq):
+    """Key 100 sits about 100 log2 units above every row's first-tile max, so every
+    wave whose rows all see it fails the fast walk's headroom from tile 1 on, and
+    whole blocks redo their rows in the safe pass.  Causal, 1536 rows: the pair
+    (rows 1280-1535, rows 0-255) fails all of its first pass and part of its second
+    (whose first wave never sees key 100).  Non-causal, 600 rows over 1536 keys:
+    every full block fails; the last block's waves past row 599 do not."""
+    g = torch.Generator().manual_seed(13)
+    b, h = 1, 2
+    sk = 1536
+    q = torch.randn(b, sq, h, d, generator=g) * 0.5 + 1.0
+    k = torch.randn(b, sk, h, d, generator=g) * 0.5
+    k[:, 100] = 104 / (1.4427 * d ** 0.5)
+    q, k = q.bfloat16().to(cuda), k.bfloat16().to(cuda)
+    v = torch.randn(b, sk, h, d, generator=g).bfloat16().to(cuda)
+    out = flash_attn_func(q, k, v, causal=causal)
+    ref = attention(values(q), values(k), values(v), d ** -0.5, causal)
+    assert_close(out, ref, torch.bfloat16, paged=False)
