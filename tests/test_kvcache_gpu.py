@@ -81,6 +81,47 @@ def test_append_either_side_of_the_fused_limit(cuda, dtype, nseqs):
     np.testing.assert_array_equal(cache_words(vc), vw)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("h", [3, 6])
+@pytest.mark.parametrize("mode", ["append", "slots"])
+def test_scatter_store_of_one_token_per_sequence(cuda, dtype, d, h, mode):
+    """Past 1024 rows, a decode's one token per sequence is stored by the scatter
+    kernel before the decode (one wave per token and head, four heads per block).
+    Head counts of 3 and 6 leave the last group of four part-empty; every head dim;
+    the append at lens, and the engine path's store at given slots (every 7th
+    sequence's slot is -1: nothing stored, and it attends its cached keys).  The
+    cache holds the bytes the layout oracle says (unwritten slots keep their NaN
+    poison) and the output matches the float64 reference."""
+    nseqs, page = -(-1100 // h), 16
+    rng = random.Random(h * 1000 + d)
+    lens = [rng.randrange(1, 40) for _ in range(nseqs)]
+    lens[:3] = [1, 15, 16]
+    q, kc, vc, bt, ks, vs = stage([n + 1 for n in lens], h, d, page, dtype, seed=h + d, device=cuda)
+    ks, vs = [k[:, :n] for k, n in zip(ks, lens)], [v[:, :n] for v, n in zip(vs, lens)]
+    kw, vw = cache_words(kc), cache_words(vc)
+    g = torch.Generator().manual_seed(d)
+    kn, vn = (torch.randn(nseqs, 1, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))
+    slots = layout.append_slots(lens, bt.cpu().numpy(), page)
+    if mode == "append":
+        seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
+        out = flash_attn_with_kvcache(q, kc, vc, k=kn, v=vn, cache_seqlens=seqlens, page_table=bt)
+        ks2, vs2 = appended(ks, vs, kn, vn)
+    else:
+        skip = set(range(0, nseqs, 7))
+        slots[sorted(skip)] = -1
+        post = torch.tensor([n if s in skip else n + 1 for s, n in enumerate(lens)], dtype=torch.int32,
+                            device=cuda)
+        out = K.module().decode(K.runtime(), q, kc, vc, kn, vn, torch.from_numpy(slots).to(cuda), post, bt,
+                                None, None)
+        ks2 = [k if s in skip else torch.cat([k, kn[s:s + 1]], 1) for s, k in enumerate(ks)]
+        vs2 = [v if s in skip else torch.cat([v, vn[s:s + 1]], 1) for s, v in enumerate(vs)]
+    assert_close(out, reference(q, ks2, vs2, d ** -0.5), dtype, paged=True)
+    layout.store(kw, vw, row_words(kn[:, 0]), row_words(vn[:, 0]), slots, page)
+    np.testing.assert_array_equal(cache_words(kc), kw)
+    np.testing.assert_array_equal(cache_words(vc), vw)
+
+
 def long_tile_waves(nseqs, h, width, page):
     """256-key tiles the decode's rows hold at the page table's capacity; the kernel
     takes 64-key tiles when this is at most 2048 (csrc/ca_decode.hip)."""
