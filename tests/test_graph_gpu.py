@@ -73,6 +73,35 @@ def test_flash_attn_with_kvcache_append_replays(cuda, dtype, no_host_checks):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+def test_large_batch_append_replays(cuda, dtype, no_host_checks):
+    """Past 1024 (sequence, head) rows the one-token append is a separate scatter
+    kernel before the decode: both dispatches inside the graph."""
+    import random
+    rng = random.Random(3)
+    lens_host = [rng.randrange(1, 60) * 2 + 1 for _ in range(300)]  # odd: never a page edge
+    q0, kc, vc, bt, _, _ = stage(lens_host, H, D, PAGE, dtype, seed=33, device=cuda)
+    b = len(lens_host)
+    assert b * H > 1024
+    lens = torch.tensor(lens_host, dtype=torch.int32, device=cuda) - 1  # the append overwrites the last
+    sq, sk, sv = (torch.zeros(b, 1, H, D, dtype=dtype, device=cuda) for _ in range(3))
+    graph, out = capture(lambda: flash_attn_with_kvcache(sq, kc, vc, k=sk, v=sv, cache_seqlens=lens,
+                                                          page_table=bt))
+    g = torch.Generator(device=cuda).manual_seed(6)
+    for _ in range(3):
+        for t in (sq, sk, sv):
+            t.copy_(torch.randn(t.shape, generator=g, device=cuda).to(dtype))
+        kr, vr = kc.clone(), vc.clone()
+        ref = flash_attn_with_kvcache(sq.clone(), kr, vr, k=sk.clone(), v=sv.clone(), cache_seqlens=lens,
+                                      page_table=bt)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all()
+        assert same_bytes(out, ref)
+        assert same_bytes(kc, kr) and same_bytes(vc, vr)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_engine_step_with_slots_and_out_replays(cuda, dtype, no_host_checks):
     """The engine entry: store each new token at ``slots`` (one sequence skips with
     -1), lens is the post-store length, the caller owns ``out``."""
