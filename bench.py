@@ -1,7 +1,7 @@
 """Benchmark of cpu-attention's hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
-                    [--no-configs] [--profile-pass] [--clock-trace N]
+                    [--no-configs] [--profile-pass] [--profile-configs] [--clock-trace N]
 
 The headline step is one call of the paged decode over BASELINE cfg3 (bf16,
 N=64 H=32 E=128 page 32, cache_seqlens U[17,2047], random-permutation page table,
@@ -293,19 +293,29 @@ def slots_for(table, lens, page, pad_frac, rng):
     return out, len(real)
 
 
-def run_configs(dev, mod, rt):
-    """The BASELINE configs other than the headline decode and prefill."""
+def run_configs(dev, mod, rt, profile_calls=0):
+    """The BASELINE configs other than the headline decode and prefill.  With
+    ``profile_calls``, nothing is timed: each config's call runs that many times
+    (cfg5's 32-step loop once), for a counter run to read."""
     from cpu_attention import flash_attn_func, flash_attn_with_kvcache, reshape_and_cache
 
     flush = Flush(dev)
     res = {}
+
+    def measure_or_run(fn, *args, **kw):
+        if not profile_calls:
+            return measure(fn, *args, **kw)
+        for _ in range(profile_calls):
+            fn()
+        torch.cuda.synchronize()
+        return {}
 
     # cfg1: prefill bf16 N=1 L=S=128 H=16 E=64 causal (latency-bound: 34 MFLOP).
     g = torch.Generator(device=dev).manual_seed(2)
     q, k, v = (torch.randn(1, 128, 16, 64, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
     flop = causal_flop(1, 16, 64, 128, 128)
     res["cfg1"] = {"workload": "flash_attn_func bf16 causal N=1 L=S=128 H=16 E=64", "algorithmic_flop": flop,
-                   **measure(lambda: flash_attn_func(q, k, v, causal=True), flush, flop, "TFLOP/s",
+                   **measure_or_run(lambda: flash_attn_func(q, k, v, causal=True), flush, flop, "TFLOP/s",
                              peak=BF16_PEAK_TFLOPS),
                    "published_cpu": PUBLISHED["cfg1"]}
     del q, k, v
@@ -327,7 +337,7 @@ def run_configs(dev, mod, rt):
                                "random-permutation page table, caches filled by reshape_and_cache, "
                                "one-token append per call",
                    "algorithmic_bytes": nbytes,
-                   **measure(lambda: flash_attn_with_kvcache(q, kc, vc, k=kn, v=vn, cache_seqlens=seqlens,
+                   **measure_or_run(lambda: flash_attn_with_kvcache(q, kc, vc, k=kn, v=vn, cache_seqlens=seqlens,
                                                              page_table=table), flush, nbytes, "GB/s",
                              peak=HBM_PEAK_GBS),
                    "published_cpu": PUBLISHED["cfg2"]}
@@ -340,7 +350,7 @@ def run_configs(dev, mod, rt):
     nbytes = 2 * q.numel() * 2 + 2 * k.numel() * 2
     res["cfg4_cross"] = {"workload": "flash_attn_func bf16 non-causal N=8 L=1 S=2048 H=32 E=32",
                          "algorithmic_bytes": nbytes,
-                         **measure(lambda: flash_attn_func(q, k, v, causal=False), flush, nbytes, "GB/s",
+                         **measure_or_run(lambda: flash_attn_func(q, k, v, causal=False), flush, nbytes, "GB/s",
                                    peak=HBM_PEAK_GBS)}
     del q, k, v
 
@@ -360,7 +370,7 @@ def run_configs(dev, mod, rt):
     res["cfg5_store"] = {"workload": f"reshape_and_cache bf16 H=32 E=128 page 16: {len(slots)} slot entries "
                                      f"({len(slots) - nreal} of them -1) for 128 prompts of U[64,1024] tokens",
                          "algorithmic_bytes": store_bytes,
-                         **measure(lambda: reshape_and_cache(key, val, kc, vc, sl), flush, store_bytes, "GB/s",
+                         **measure_or_run(lambda: reshape_and_cache(key, val, kc, vc, sl), flush, store_bytes, "GB/s",
                                    steps=30, warmup=3, cold_samples=10, peak=HBM_PEAK_GBS, api_calls=20)}
     del key, val
     qs = torch.randn(nsteps, n, 1, h, e, generator=g, device=dev).to(torch.bfloat16)
@@ -373,6 +383,10 @@ def run_configs(dev, mod, rt):
         for s in range(nsteps):
             flash_attn_with_kvcache(qs[s], kc, vc, k=ks[s], v=vs[s], cache_seqlens=lens_t[s], page_table=table)
 
+    if profile_calls:
+        loop()
+        torch.cuda.synchronize()
+        return res
     nramp = ramp(loop, 0.05)
     loop()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nsteps)]
@@ -548,6 +562,21 @@ def profile_pass(dev, mod, rt, calls=5):
     print("profile pass done", flush=True)
 
 
+def profile_configs(dev, mod, rt, calls=5):
+    """No timing: one 1 GiB device copy (the counters' calibration), then `calls`
+    calls of each other BASELINE config (cfg1, cfg2, cfg4's cross shape, cfg5's
+    staging store) and one pass of cfg5's 32 append+decode steps."""
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+    run_configs(dev, mod, rt, profile_calls=calls)
+    print("profile configs done", flush=True)
+
+
 def clock_trace(dev, mod, rt, calls):
     """`calls` back-to-back prefill calls (cfg4) from a cold start, each bracketed by
     events: one line per call (index, µs), then a summary."""
@@ -588,6 +617,9 @@ def main():
     ap.add_argument("--profile-pass", action="store_true",
                     help="no timing: one 1 GiB device copy, then a few decode and prefill calls "
                          "(for rocprofv3 --pmc runs)")
+    ap.add_argument("--profile-configs", action="store_true",
+                    help="no timing: one 1 GiB device copy, then a few calls of each other config "
+                         "(for rocprofv3 --pmc runs)")
     ap.add_argument("--clock-trace", type=int, default=0, metavar="N",
                     help="print the event time of N back-to-back prefill calls from a cold start")
     args = ap.parse_args()
@@ -607,6 +639,9 @@ def main():
 
     if args.profile_pass:
         profile_pass(dev, mod, rt)
+        return
+    if args.profile_configs:
+        profile_configs(dev, mod, rt)
         return
     if args.clock_trace:
         clock_trace(dev, mod, rt, args.clock_trace)
