@@ -82,6 +82,7 @@ def flash(q, k, v, scale, causal, bf16, threads=0):
     """q [B, L, H, E], k/v [B, S, H, E] element arrays (float32 or uint16 bf16
     bits, any strides numpy allows).  Returns the output [B, L, H, E]."""
     b, sq, heads, hd = q.shape
+    assert hd % 16 == 0, "the C port tiles head_dim by 16"
     sk = k.shape[1]
     es = q.itemsize
     qs, ks, vs = ((ctypes.c_int64 * 3)(*[s // es for s in x.strides[:3]]) for x in (q, k, v))

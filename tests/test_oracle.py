@@ -283,7 +283,10 @@ def test_cport_decode_against_float64(dtype, page):
 @pytest.mark.parametrize("dtype", [FP32, BF16])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("sq,sk", [(1, 1), (37, 100), (100, 37), (129, 129)])
-def test_cport_flash_against_float64(dtype, causal, sq, sk):
+@pytest.mark.parametrize("tiles", ["host", "avx2"])
+def test_cport_flash_against_float64(dtype, causal, sq, sk, tiles, monkeypatch):
+    if tiles == "avx2":  # the AVX2 tiles, whatever the host has
+        monkeypatch.setenv("CA_ORACLE_AVX2", "1")
     rng = np.random.default_rng(sq * 7 + sk)
     b, h, hd = 2, 3, 64
     q, k, v = (rng.standard_normal((b, n, h, hd)).astype(np.float32) for n in (sq, sk, sk))
