@@ -261,7 +261,7 @@ def _flash(q, k, v, softmax_scale, causal):
     rt, _, flash = _ENTRIES or _entries()
     out = flash(rt, q, k, v, softmax_scale, causal, 0, 0)
     if type(out) is int:
-        # The few-rows route asked for split-K scratch (an int = the bytes it
+        # A call whose keys are split over blocks asked for scratch (an int = the bytes it
         # needs).  It is allocated for this call on the current stream: the
         # caching allocator hands the bytes to nothing else until the kernels
         # queued on that stream have used them, and under graph capture the

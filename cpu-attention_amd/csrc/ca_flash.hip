@@ -277,8 +277,8 @@ struct Bf16Rows {
 
   // Keys of tile t this lane's row may see: key 32kt + 8(r/4) + 4hf + r%4 of the
   // tile is visible when 32kt + 8(r/4) + r%4 <= the returned limit.
-  __device__ __forceinline__ int vis_of(const Bf16Pass& a, int t) const {
-    const int k0 = t * BN;
+  __device__ __forceinline__ int vis_of(const Bf16Pass& a, int kbeg, int t) const {
+    const int k0 = kbeg + t * BN;
     int lim = a.S - 1 - k0;
     if (a.causal) lim = min(lim, r0 + li + a.diag - k0);
     return max(-1, min(lim, BN)) - 4 * hf;
@@ -345,6 +345,29 @@ struct Bf16Rows {
 #pragma unroll
       for (int d = 0; d < ND; ++d)
         o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_operand<E>(vb, lane, cc, d), pb[cc], o[d], 0, 0, 0);
+  }
+
+  // The rows' partial for the combine (keys split over blocks): O^T unnormalised,
+  // the running max (scaled log2 units) and l, at slot slot0 + row * splits of
+  // the workspace.  A row that saw no key leaves m = -inf, l = 0, O = 0.
+  __device__ __forceinline__ void store_partial(const Bf16Pass& a, float* pacc, float* pml, int64_t slot0,
+                                                int splits) const {
+    const float lt = l + __shfl_xor(l, 32);
+    const int row = r0 + li;
+    if (row < a.L) {
+      const int64_t slot = slot0 + (int64_t)row * splits;
+      float* orow = pacc + slot * E;
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f32x4*>(orow + 32 * d + 8 * q + 4 * hf) =
+              f32x4{o[d][4 * q], o[d][4 * q + 1], o[d][4 * q + 2], o[d][4 * q + 3]};
+      if (hf == 0) {
+        pml[2 * slot] = m;
+        pml[2 * slot + 1] = lt;
+      }
+    }
   }
 
   // out = acc / l; a row with no visible key is 0.
@@ -483,14 +506,14 @@ struct P64Rows {
       for (int d = 0; d < ND; ++d) asm volatile("" : "+a"(o[cb][d]));
   }
 
-  // Keys of tile t row (cb, li) may see: key 32kt + 8(r/4) + 4hf + r%4 of the
-  // tile is visible when 32kt + 8(r/4) + r%4 <= the returned limit.
-  // The lane id is recomputed here (this runs only on masked tiles), so that no
-  // register holds a lane constant for it across the walk.
-  __device__ __forceinline__ int vis_of(const Bf16Pass& a, int t, int cb) const {
+  // Keys of tile t (from key kbeg on) row (cb, li) may see: key 32kt + 8(r/4) +
+  // 4hf + r%4 of the tile is visible when 32kt + 8(r/4) + r%4 <= the returned
+  // limit.  The lane id is recomputed here (this runs only on masked tiles), so
+  // that no register holds a lane constant for it across the walk.
+  __device__ __forceinline__ int vis_of(const Bf16Pass& a, int kbeg, int t, int cb) const {
     int lid;
     asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lid));
-    const int k0 = t * BN;
+    const int k0 = kbeg + t * BN;
     int lim = a.S - 1 - k0;
     if (a.causal) lim = min(lim, r0 + 32 * cb + (lid & 31) + a.diag - k0);
     return max(-1, min(lim, BN)) - 4 * (lid >> 5);
@@ -515,10 +538,10 @@ struct P64Rows {
   // fixed assembly block per logit with a single temporary (the compiler would
   // interleave the elements and run out of registers on this rare path).
   template <int PAR>
-  __device__ __forceinline__ void apply_mask(const Bf16Pass& a, int t) {
+  __device__ __forceinline__ void apply_mask(const Bf16Pass& a, int kbeg, int t) {
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      const int vis = vis_of(a, t, cb);
+      const int vis = vis_of(a, kbeg, t, cb);
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -700,14 +723,63 @@ struct P64Rows {
       }
     }
   }
+
+  // Bytes of LDS that store_partials needs per wave: 32 rows of E floats, padded.
+  static constexpr int kPartRow = 4 * E + 16;
+  static constexpr int kPartBytes = 32 * kPartRow;
+
+  // The rows' partial for the combine (keys split over blocks): O^T unnormalised
+  // (fp32), the fixed max m (scaled log2 units) and l, at slot slot0 + row *
+  // splits of the workspace, staged through this wave's `stage` area as
+  // store_staged stages the output (each store instruction writes 256 / E whole
+  // rows).  A row that saw no key leaves m = -inf, l = 0, O = 0.
+  __device__ __forceinline__ void store_partials(const Bf16Pass& a, char* stage, float* pacc, float* pml,
+                                                 int64_t slot0, int splits) {
+    constexpr int CPR = E / 4, RPI = 64 / CPR;  // 16-byte chunks per row, rows per store
+    mfma_guard();
+    const int ch = lane % CPR, rr0 = lane / CPR;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const float lt = l[cb] + __shfl_xor(l[cb], 32);
+      const int rowl = r0 + 32 * cb + li;
+      if (hf == 0 && rowl < a.L) {
+        const int64_t slot = slot0 + (int64_t)rowl * splits;
+        pml[2 * slot] = m[cb];
+        pml[2 * slot + 1] = lt;
+      }
+      char* rowp = stage + li * kPartRow;
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f32x4*>(rowp + (32 * d + 8 * q + 4 * hf) * 4) =
+              f32x4{o[cb][d][4 * q], o[cb][d][4 * q + 1], o[cb][d][4 * q + 2], o[cb][d][4 * q + 3]};
+#pragma unroll
+      for (int k = 0; k < 32 / RPI; ++k) {
+        const int rr = rr0 + RPI * k, row = r0 + 32 * cb + rr;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(stage + rr * kPartRow + ch * 16);
+        if (row < a.L) *reinterpret_cast<f32x4*>(pacc + (slot0 + (int64_t)row * splits) * E + ch * 4) = v;
+      }
+    }
+  }
 };
 
 // The safe pass of the 64-row kernel: both column blocks of every wave walk the
 // pass with a lazily refreshed running max (as bf16_safe_pass), one tile buffer
 // each for K and V, loaded by all 4 waves.  Waves with `active` false compute and
 // store nothing but take part in the loads and barriers.
-template <int E>
-__device__ __noinline__ void bf16_safe_pass_p64(const Bf16Pass& a, bool active) {
+// The split mode's pass: its keys start at kbeg, and its rows' partials go to
+// slots slot0 + row * splits of the workspace.
+struct SplitOut {
+  float* pacc;
+  float* pml;
+  int64_t slot0;
+  int splits;
+  int kbeg;
+};
+
+template <int E, bool SPLIT>
+__device__ __forceinline__ void bf16_safe_pass_body(const Bf16Pass& a, bool active, const SplitOut* so) {
   using C = FlashP64Cfg<E>;
   constexpr int BN = C::BN, ND = E / 32, NL = C::NL;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
@@ -718,10 +790,13 @@ __device__ __noinline__ void bf16_safe_pass_p64(const Bf16Pass& a, bool active) 
   int koff[NL], voff[NL];
   tile_offsets<E, FlashBf16Cfg<E>::RSK>(wv, lane, a.ks1, koff);
   tile_offsets<E, FlashBf16Cfg<E>::RSV>(wv, lane, a.vs1, voff);
+  // The pass's keys [kbeg, a.kend): all it sees, or the block's split of them.
+  int kbeg = 0;
+  if constexpr (SPLIT) kbeg = so->kbeg;
   TileStream<E> tk, tv;
-  tk.init(a.k, a.ks1, a.kend, Ks, 1, 0, wv);
-  tv.init(a.v, a.vs1, a.kend, Vs, 1, 0, wv);
-  const int nkt = a.kend > 0 ? (a.kend + BN - 1) / BN : 0;
+  tk.init(a.k + (int64_t)kbeg * a.ks1, a.ks1, a.kend - kbeg, Ks, 1, 0, wv);
+  tv.init(a.v + (int64_t)kbeg * a.vs1, a.vs1, a.kend - kbeg, Vs, 1, 0, wv);
+  const int nkt = a.kend > kbeg ? (a.kend - kbeg + BN - 1) / BN : 0;
   Bf16Rows<E> w[2];
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
@@ -738,12 +813,12 @@ __device__ __noinline__ void bf16_safe_pass_p64(const Bf16Pass& a, bool active) 
     loads_done_barrier();
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      const int kend_w = a.causal ? min(a.S, w[cb].r0 + 32 + a.diag) : a.S;
-      const int nkt_w = active && kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
+      const int kend_w = min(a.causal ? min(a.S, w[cb].r0 + 32 + a.diag) : a.S, a.kend);
+      const int nkt_w = active && kend_w > kbeg ? (kend_w - kbeg + BN - 1) / BN : 0;
       if (t < nkt_w) {
         f32x16 st[2];
         w[cb].logits(Ks, st);
-        const int vis = w[cb].vis_of(a, t);
+        const int vis = w[cb].vis_of(a, kbeg, t);
         const float mt = w[cb].tile_max(st, vis, a.c);
         if (__any(mt > w[cb].m + 8.f)) {
           const float mn = fmaxf(w[cb].m, mt);
@@ -761,12 +836,34 @@ __device__ __noinline__ void bf16_safe_pass_p64(const Bf16Pass& a, bool active) 
     __syncthreads();  // every wave is done with the tiles before they are refilled
   }
   if (active) {
-    w[0].store(a);
-    w[1].store(a);
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) w[cb].store_partial(a, so->pacc, so->pml, so->slot0, so->splits);
+    } else {
+      w[0].store(a);
+      w[1].store(a);
+    }
   }
 }
 
+// The safe pass out of line: for the output, or for the split mode's partials
+// (the slots are passed in: a called function cannot read the kernel's
+// arguments itself).
 template <int E>
+__device__ __noinline__ void bf16_safe_pass_p64(const Bf16Pass& a, bool active) {
+  bf16_safe_pass_body<E, false>(a, active, nullptr);
+}
+template <int E>
+__device__ __noinline__ void bf16_safe_pass_p64(const Bf16Pass& a, bool active, const SplitOut& so) {
+  bf16_safe_pass_body<E, true>(a, active, &so);
+}
+
+// SPLIT: the keys of each query block are split over gridDim.y blocks (calls whose
+// query blocks leave most CUs idle); each block walks its range of whole key
+// tiles and leaves (O, m, l) partials per row in the workspace for the combine
+// kernel.  Otherwise a block takes a causal pair or a query block and writes the
+// output.
+template <int E, bool SPLIT>
 __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
   using C = FlashP64Cfg<E>;
   constexpr int BM = C::BM, BN = C::BN, NL = C::NL;
@@ -776,7 +873,20 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const PairWork pw = pair_work(p, BM);
+  PairWork pw;
+  int sp = 0, splits = 1;
+  if constexpr (SPLIT) {
+    const int64_t nqb = cdiv(p.seq_q, BM);
+    const int64_t bh = blockIdx.x / nqb;
+    pw.b = bh / p.heads;
+    pw.h = bh - pw.b * p.heads;
+    pw.qb0 = pw.qb1 = blockIdx.x - bh * nqb;
+    pw.n = 1;
+    sp = blockIdx.y;
+    splits = gridDim.y;
+  } else {
+    pw = pair_work(p, BM);
+  }
   // Positions and token strides fit 32 bits (the launcher declines otherwise).
   Bf16Pass a;
   a.L = (int)p.seq_q;
@@ -805,10 +915,18 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
   for (int pass = 0; pass < pw.n; ++pass) {
     const int q0 = (int)(pass == 0 ? pw.qb0 : pw.qb1) * BM;
     w.r0 = q0 + 64 * wv;
-    const int kend_b = p.causal ? min(S, q0 + BM + diag) : S;
-    const int nkt = kend_b > 0 ? (kend_b + BN - 1) / BN : 0;
-    const int kend_w = p.causal ? min(S, w.r0 + 64 + diag) : S;
-    const int nkt_w = kend_w > 0 ? (kend_w + BN - 1) / BN : 0;
+    // The pass's keys [kbeg, kend_b): all it sees, or this block's split of them
+    // (whole tiles; a split past the pass's last key is empty).
+    int kbeg = 0, kend_b = p.causal ? min(S, q0 + BM + diag) : S;
+    if constexpr (SPLIT) {
+      const int chunk = (int)cdiv(cdiv(p.seq_k, BN), splits) * BN;
+      kbeg = min(sp * chunk, max(kend_b, 0));
+      kend_b = min(kbeg + chunk, kend_b);
+    }
+    const int nkt = kend_b > kbeg ? (kend_b - kbeg + BN - 1) / BN : 0;
+    int kend_w = p.causal ? min(S, w.r0 + 64 + diag) : S;
+    if constexpr (SPLIT) kend_w = min(kend_w, kend_b);
+    const int nkt_w = kend_w > kbeg ? (kend_w - kbeg + BN - 1) / BN : 0;
     a.q0 = q0;
     a.kend = kend_b;
 
@@ -825,8 +943,8 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
     // issues it, and every tile is read only after a barrier that follows its
     // landing.
     TileStream<E> tk, tv;
-    tk.init(a.k, a.ks1, kend_b, Ks, C::NBUFK, 0, wv);
-    tv.init(a.v, a.vs1, kend_b, Vs, C::NBUFV, 0, wv);
+    tk.init(a.k + (int64_t)kbeg * a.ks1, a.ks1, kend_b - kbeg, Ks, C::NBUFK, 0, wv);
+    tv.init(a.v + (int64_t)kbeg * a.vs1, a.vs1, kend_b - kbeg, Vs, C::NBUFV, 0, wv);
     if (nkt > 0) {
       tk.issue(koff);
       tk.issue(koff);
@@ -844,7 +962,7 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
       };
       // A tile needs the key limits when a row of the wave ends inside it.
       auto masked = [&](int t) __attribute__((always_inline)) {
-        const int k0 = t * BN;
+        const int k0 = kbeg + t * BN;
         return k0 + BN > S || (p.causal && k0 + BN - 1 > w.r0 + diag);
       };
       int t = 0;
@@ -855,7 +973,7 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
         // for the safe pass), then the softmax of tile 0 beside the S of tile 1.
         w.template step<1, false, true, false>(Vs, kbuf(0), a.c, [] {});
         P64Rows<E>::mfma_guard();
-        w.template apply_mask<0>(a, 0);
+        w.template apply_mask<0>(a, kbeg, 0);
         w.fix_max(a.c);
         bad |= !w.template step<0, false, true, true>(Vs, kbuf(1), a.c, loads);
         loads_landed_barrier<2 * NL>();
@@ -864,7 +982,7 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
         // of a tile it does not use).
         auto body = [&](auto par_tag, int tt) __attribute__((always_inline)) {
           constexpr int PAR = decltype(par_tag)::value;
-          if (masked(tt)) w.template apply_mask<PAR>(a, tt);
+          if (masked(tt)) w.template apply_mask<PAR>(a, kbeg, tt);
           bad |= !w.template step<PAR, true, true, true>(vbuf(tt + C::NBUFV - 1), kbuf(tt + 1), a.c, loads);
           loads_landed_barrier<2 * NL>();
         };
@@ -893,8 +1011,20 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
     bad = __any(bad);
     const bool any_bad = __syncthreads_or(bad);
     static_assert(C::NW * P64Rows<E>::kStageBytes <= C::LDS_BYTES, "the staging areas fit the tile buffers");
-    if (!bad) w.store_staged(a, reinterpret_cast<char*>(smem) + wv * P64Rows<E>::kStageBytes);
-    if (any_bad) bf16_safe_pass_p64<E>(a, bad);
+    static_assert(C::NW * P64Rows<E>::kPartBytes <= C::LDS_BYTES, "the partials' staging fits the tile buffers");
+    if constexpr (SPLIT) {
+      const int64_t slot0 = (pw.b * p.heads + pw.h) * p.seq_q * splits + sp;
+      if (!bad)
+        w.store_partials(a, reinterpret_cast<char*>(smem) + wv * P64Rows<E>::kPartBytes, p.part_acc, p.part_ml,
+                         slot0, splits);
+      if (any_bad) {
+        const SplitOut so{p.part_acc, p.part_ml, slot0, splits, kbeg};
+        bf16_safe_pass_p64<E>(a, bad, so);
+      }
+    } else {
+      if (!bad) w.store_staged(a, reinterpret_cast<char*>(smem) + wv * P64Rows<E>::kStageBytes);
+      if (any_bad) bf16_safe_pass_p64<E>(a, bad);
+    }
   }
 }
 
@@ -1066,14 +1196,15 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
 }
 
 template <typename K>
-static int launch_lds(K kernel, int64_t nb, int threads, int lds, const FlashParams& p, hipStream_t stream) {
-  if (nb > 0x7fffffff) return CA_DECLINED;
+static int launch_lds(K kernel, int64_t nb, int threads, int lds, const FlashParams& p, hipStream_t stream,
+                      int64_t ny = 1) {
+  if (nb > 0x7fffffff || ny > 0xffff) return CA_DECLINED;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return CA_HIP_ERROR - (int)e;
   }
-  hipLaunchKernelGGL(kernel, dim3((unsigned)nb), dim3(threads), lds, stream, p);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)nb, (unsigned)ny), dim3(threads), lds, stream, p);
   return ca_launch_status();
 }
 
@@ -1091,13 +1222,29 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
   if (p.seq_q >= ((int64_t)1 << 30) || p.seq_k >= ((int64_t)1 << 30)) return CA_DECLINED;
   if (rows_route(p.seq_q, bf16 != 0)) return flash_rows_launch(p, E, bf16, stream);
   if (bf16) {
-    // One block per (batch, head) and query-block pair (causal) or query block.
     const int64_t nqb = cdiv(p.seq_q, FlashP64Cfg<128>::BM);
+    const int64_t splits = tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, true);
+    if (splits > 1) {
+      // One block per (batch, head, query block) and split of its keys, then the
+      // combine of each row's partials into the output.
+      const int64_t need = tiled_workspace_bytes(p.batch, p.seq_q, p.seq_k, p.heads, E, true);
+      if (p.part_acc == nullptr || p.part_ml == nullptr || p.workspace_bytes < need) return CA_DECLINED;
+      const int64_t nb = p.batch * p.heads * nqb;
+      int st = CA_DECLINED;
+      switch (E) {
+        case 32: st = launch_lds(flash_bf16_p64_kernel<32, true>, nb, 64 * FlashP64Cfg<32>::NW, FlashP64Cfg<32>::LDS_BYTES, p, stream, splits); break;
+        case 64: st = launch_lds(flash_bf16_p64_kernel<64, true>, nb, 64 * FlashP64Cfg<64>::NW, FlashP64Cfg<64>::LDS_BYTES, p, stream, splits); break;
+        case 128: st = launch_lds(flash_bf16_p64_kernel<128, true>, nb, 64 * FlashP64Cfg<128>::NW, FlashP64Cfg<128>::LDS_BYTES, p, stream, splits); break;
+      }
+      if (st != CA_OK) return st;
+      return flash_combine_launch(p, E, bf16, splits, stream);
+    }
+    // One block per (batch, head) and query-block pair (causal) or query block.
     const int64_t nb = p.batch * p.heads * (p.causal ? (nqb + 1) / 2 : nqb);
     switch (E) {
-      case 32: return launch_lds(flash_bf16_p64_kernel<32>, nb, 64 * FlashP64Cfg<32>::NW, FlashP64Cfg<32>::LDS_BYTES, p, stream);
-      case 64: return launch_lds(flash_bf16_p64_kernel<64>, nb, 64 * FlashP64Cfg<64>::NW, FlashP64Cfg<64>::LDS_BYTES, p, stream);
-      case 128: return launch_lds(flash_bf16_p64_kernel<128>, nb, 64 * FlashP64Cfg<128>::NW, FlashP64Cfg<128>::LDS_BYTES, p, stream);
+      case 32: return launch_lds(flash_bf16_p64_kernel<32, false>, nb, 64 * FlashP64Cfg<32>::NW, FlashP64Cfg<32>::LDS_BYTES, p, stream);
+      case 64: return launch_lds(flash_bf16_p64_kernel<64, false>, nb, 64 * FlashP64Cfg<64>::NW, FlashP64Cfg<64>::LDS_BYTES, p, stream);
+      case 128: return launch_lds(flash_bf16_p64_kernel<128, false>, nb, 64 * FlashP64Cfg<128>::NW, FlashP64Cfg<128>::LDS_BYTES, p, stream);
     }
   } else {
     const int64_t nb = p.batch * p.heads * cdiv(p.seq_q, kBM);

@@ -58,7 +58,8 @@ struct FlashParams {
   int64_t qs[3], ks[3], vs[3];  // batch, token, head strides (elements)
   float c;                      // softmax scale * log2(e)
   int causal;
-  // Few-rows route only: split-K partials in the caller's workspace.
+  // Split-K partials in the caller's workspace (few-rows route, and the bf16
+  // tiled kernel's split mode).
   float* part_acc;              // [batch*heads*seq_q, splits, E]
   float* part_ml;               // [batch*heads*seq_q, splits, 2]: max (scaled log2 units), sum
   int64_t workspace_bytes;
@@ -73,6 +74,34 @@ __host__ __device__ inline bool rows_route(int64_t seq_q, bool bf16) { return se
 constexpr int kRowsWaves = 8;                 // waves per block
 constexpr int64_t kRowsTargetBlocks = 256;    // blocks that keep every CU streaming
 constexpr int64_t kRowsMaxSplits = 64;
+
+// The bf16 tiled prefill splits each query block's keys over several blocks when
+// its query blocks (batch x heads x ceil(seq_q / 256)) leave the chip's CUs short
+// of blocks: about kTiledTargetBlocks blocks, at least kTiledMinTiles key tiles
+// of 64 per split, at most kTiledMaxSplits.  Such calls (few rows over long key
+// ranges) are bound by reading K and V; with one block per query block a block's
+// serial walk over every key tile is the whole call's time.  The decision does
+// not look at `causal`, so the workspace query need not know it.
+constexpr int64_t kTiledTargetBlocks = 256;
+constexpr int64_t kTiledMinTiles = 4;
+constexpr int64_t kTiledMaxSplits = 64;
+__host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads,
+                                                bool bf16) {
+  if (!bf16 || rows_route(seq_q, bf16)) return 1;
+  const int64_t items = batch * heads * ((seq_q + 255) / 256);
+  if (items <= 0 || items >= kTiledTargetBlocks) return 1;
+  int64_t s = (kTiledTargetBlocks + items - 1) / items;
+  const int64_t by_tiles = (seq_k + 63) / 64 / kTiledMinTiles;
+  s = s < by_tiles ? s : by_tiles;
+  s = s < kTiledMaxSplits ? s : kTiledMaxSplits;
+  return s < 2 ? 1 : s;
+}
+// Workspace bytes of the split mode: (O[E], m, l) per row and split.
+__host__ __device__ inline int64_t tiled_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k,
+                                                         int64_t heads, int E, bool bf16) {
+  const int64_t s = tiled_splits(batch, seq_q, seq_k, heads, bf16);
+  return s > 1 ? batch * heads * seq_q * s * (E + 2) * 4 : 0;
+}
 
 // The decode kernel does a one-token append itself (rather than a store kernel
 // launched before it) for batches of up to this many rows (sequences x heads).
@@ -96,5 +125,7 @@ int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, 
                                    bool bf16);
 void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int head_dim, bool bf16);
 int flash_rows_launch(const FlashParams& p, int head_dim, int bf16, hipStream_t stream);
+// Merges each row's `splits` partials (p.part_acc / p.part_ml) into p.out.
+int flash_combine_launch(const FlashParams& p, int head_dim, int bf16, int64_t splits, hipStream_t stream);
 
 }  // namespace ca

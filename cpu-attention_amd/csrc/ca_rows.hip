@@ -592,10 +592,11 @@ static int64_t rows_call_splits(const FlashParams& p, int E, bool bf16) {
 }
 
 // The workspace a call of these shapes may need: its strides are not known
-// here, so the larger of the two routes' partials.
+// here, so the larger of the two routes' partials; past the few-rows route, the
+// tiled kernel's split mode.
 int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, int E,
                                    bool bf16) {
-  if (!rows_route(seq_q, bf16)) return 0;
+  if (!rows_route(seq_q, bf16)) return tiled_workspace_bytes(batch, seq_q, seq_k, heads, E, bf16);
   int64_t splits = rows_splits(batch, seq_q, seq_k, heads, E, bf16);
   if (rows_heads_shapes(seq_q, seq_k, heads, E, bf16)) {
     const int64_t hs = rows_heads_splits(batch, seq_k, heads, E, bf16);
@@ -606,7 +607,8 @@ int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, 
 }
 
 void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int E, bool bf16) {
-  const int64_t splits = rows_call_splits(p, E, bf16);
+  const int64_t splits = rows_route(p.seq_q, bf16) ? rows_call_splits(p, E, bf16)
+                                                   : tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, bf16);
   p.part_acc = static_cast<float*>(ws);
   p.part_ml = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.batch * p.heads * p.seq_q * splits * E * 4)
                  : nullptr;
@@ -634,6 +636,28 @@ static int rows_launch_t(const FlashParams& p, hipStream_t stream) {
   const int64_t rows = p.batch * p.heads * p.seq_q;
   hipLaunchKernelGGL((flash_rows_combine_kernel<E, BF>), dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, stream, p,
                      (int)splits);
+  return ca_launch_status();
+}
+
+int flash_combine_launch(const FlashParams& p, int E, int bf16, int64_t splits, hipStream_t stream) {
+  const int64_t rows = p.batch * p.heads * p.seq_q;
+  if (cdiv(rows, 4) > 0x7fffffff) return CA_DECLINED;
+  const dim3 grid((unsigned)cdiv(rows, 4));
+  if (bf16) {
+    switch (E) {
+      case 32: hipLaunchKernelGGL((flash_rows_combine_kernel<32, true>), grid, dim3(256), 0, stream, p, (int)splits); break;
+      case 64: hipLaunchKernelGGL((flash_rows_combine_kernel<64, true>), grid, dim3(256), 0, stream, p, (int)splits); break;
+      case 128: hipLaunchKernelGGL((flash_rows_combine_kernel<128, true>), grid, dim3(256), 0, stream, p, (int)splits); break;
+      default: return CA_DECLINED;
+    }
+  } else {
+    switch (E) {
+      case 32: hipLaunchKernelGGL((flash_rows_combine_kernel<32, false>), grid, dim3(256), 0, stream, p, (int)splits); break;
+      case 64: hipLaunchKernelGGL((flash_rows_combine_kernel<64, false>), grid, dim3(256), 0, stream, p, (int)splits); break;
+      case 128: hipLaunchKernelGGL((flash_rows_combine_kernel<128, false>), grid, dim3(256), 0, stream, p, (int)splits); break;
+      default: return CA_DECLINED;
+    }
+  }
   return ca_launch_status();
 }
 

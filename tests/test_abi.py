@@ -134,7 +134,7 @@ def test_flash_workspace_for_few_rows(dtype, d, chunk):
 
     def expect(b, sq, sk, h):
         if sq > (4 if dtype == 1 else 16):
-            return 0
+            return tiled(b, sq, sk, h, d, dtype)
         blocks = b * h * -(-sq // (1 if sq == 1 else 4))
         splits = 1 if blocks >= 256 else -(-256 // blocks)
         splits = max(1, min(splits, -(-(-(-sk // chunk)) // 8), 64))
@@ -146,9 +146,36 @@ def test_flash_workspace_for_few_rows(dtype, d, chunk):
     assert lib.ca_flash_workspace_bytes(1, 1, 100000, 1, d, dtype) == 1 * 1 * 1 * 64 * (d + 2) * 4
     assert lib.ca_flash_workspace_bytes(8, 1, 2048, 32, d, dtype) == 0  # 256 blocks fill the chip
     assert lib.ca_flash_workspace_bytes(3, 4, 8 * chunk, 5, d, dtype) == 0  # one chunk per wave
-    assert lib.ca_flash_workspace_bytes(3, 17, 5000, 5, d, dtype) == 0  # the tiled route
-    assert (lib.ca_flash_workspace_bytes(1, 5, 50000, 1, d, dtype) == 0) == (dtype == 1)  # bf16: tiled
+    assert lib.ca_flash_workspace_bytes(3, 17, 5000, 5, d, dtype) == tiled(3, 17, 5000, 5, d, dtype)
+    assert lib.ca_flash_workspace_bytes(1, 5, 50000, 1, d, dtype) > 0  # bf16: tiled split; fp32: few rows
     assert lib.ca_flash_workspace_bytes(3, 4, 5000, 5, 48, dtype) == 0  # head_dim
+
+
+def tiled(b, sq, sk, h, d, dtype):
+    """The bf16 tiled prefill's split mode: when its query blocks (b * h *
+    ceil(sq / 256)) number fewer than 256, each one's keys are split over about
+    256 / blocks blocks, at least 4 key tiles of 64 each and at most 64 splits,
+    which needs (E + 2) floats per (batch, head, row, split).  fp32 never splits."""
+    if dtype != 1:
+        return 0
+    blocks = b * h * -(-sq // 256)
+    if blocks >= 256:
+        return 0
+    splits = min(-(-256 // blocks), -(-sk // 64) // 4, 64)
+    return 0 if splits < 2 else b * h * sq * splits * (d + 2) * 4
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_flash_workspace_for_split_keys(d):
+    lib = K.load_library()
+    for b, sq, sk, h in ((1, 64, 4096, 32), (1, 17, 2100, 8), (2, 300, 1500, 4), (4, 4096, 4096, 32),
+                         (1, 128, 128, 16), (1, 600, 255, 3), (1, 5, 100000, 1)):
+        assert lib.ca_flash_workspace_bytes(b, sq, sk, h, d, 1) == tiled(b, sq, sk, h, d, 1)
+        if sq > 16:  # fp32 past the few-rows route: the tiled kernel never splits
+            assert lib.ca_flash_workspace_bytes(b, sq, sk, h, d, 0) == 0
+    assert lib.ca_flash_workspace_bytes(1, 64, 4096, 32, d, 1) == 32 * 64 * 8 * (d + 2) * 4  # 8 splits
+    assert lib.ca_flash_workspace_bytes(4, 4096, 4096, 32, d, 1) == 0  # cfg4: 2048 query blocks
+    assert lib.ca_flash_workspace_bytes(1, 128, 128, 16, d, 1) == 0  # cfg1: 2 key tiles
 
 
 def test_missing_library_is_a_loud_error(monkeypatch):

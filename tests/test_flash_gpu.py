@@ -215,3 +215,65 @@ def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq):
     out = flash_attn_func(q, k, v, causal=causal)
     ref = attention(values(q), values(k), values(v), d ** -0.5, causal)
     assert_close(out, ref, torch.bfloat16, paged=False)
+
+
+# Calls whose query blocks leave most CUs idle split each query block's keys over
+# several blocks (split mode of the bf16 tiled kernel): (batch, seq_q, seq_k, heads).
+SPLIT_SHAPES = [(1, 64, 4096, 32), (1, 17, 2100, 8), (2, 300, 1500, 4), (1, 600, 4000, 3)]
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", SPLIT_SHAPES)
+def test_split_keys(cuda, d, causal, shape):
+    """Few query rows over long key ranges, so the keys of each query block are
+    split over several blocks and the row partials merged by the combine kernel:
+    unequal lengths, partial last tiles and query blocks, causal ranges that end
+    inside a split and splits past a query block's last key."""
+    b, sq, sk, h = shape
+    run(b, sq, sk, h, d, torch.bfloat16, causal, 31 + sq, cuda)
+
+
+def test_split_keys_rows_without_keys(cuda):
+    """Causal with more query rows than keys: the first rows see no key (exactly 0)
+    in every split."""
+    g = torch.Generator().manual_seed(32)
+    q = torch.randn(1, 700, 4, 64, generator=g).bfloat16().to(cuda)
+    k, v = (torch.randn(1, 600, 4, 64, generator=g).bfloat16().to(cuda) for _ in range(2))
+    out = flash_attn_func(q, k, v, causal=True)
+    assert torch.count_nonzero(out[:, :100]) == 0
+    ref = attention(values(q), values(k), values(v), 64 ** -0.5, True)
+    assert_close(out, ref, torch.bfloat16, paged=False)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_split_keys_safe_pass(cuda, d):
+    """A key about 100 log2 units above its split's first tile: the waves of the
+    split that holds it redo their rows in the safe pass, which writes partials
+    for the combine like the fast walk."""
+    g = torch.Generator().manual_seed(33)
+    b, sq, sk, h = 1, 64, 4096, 8
+    q = torch.randn(b, sq, h, d, generator=g) * 0.5 + 1.0
+    k = torch.randn(b, sk, h, d, generator=g) * 0.5
+    k[:, 2100] = 104 / (1.4427 * d ** 0.5)
+    q, k = q.bfloat16().to(cuda), k.bfloat16().to(cuda)
+    v = torch.randn(b, sk, h, d, generator=g).bfloat16().to(cuda)
+    for causal in (False, True):
+        out = flash_attn_func(q, k, v, causal=causal)
+        ref = attention(values(q), values(k), values(v), d ** -0.5, causal)
+        assert_close(out, ref, torch.bfloat16, paged=False)
+
+
+def test_split_keys_module_asks_for_workspace(cuda):
+    """The native module's flash returns the workspace bytes a split call needs when
+    it gets less (the reference's grow-and-retry, flash_attn_interface.py:186-193)."""
+    from cpu_attention import _kernel as K
+    mod = K.module()
+    q = torch.randn(1, 64, 32, 128, device=cuda).bfloat16()
+    k = torch.randn(1, 4096, 32, 128, device=cuda).bfloat16()
+    need = mod.flash(K.runtime(), q, k, k, None, False, None, 0)
+    assert isinstance(need, int) and need == 32 * 64 * 8 * 130 * 4
+    ws = torch.empty(need, dtype=torch.uint8, device=cuda)
+    out = mod.flash(K.runtime(), q, k, k, None, False, ws.data_ptr(), need)
+    ref = attention(values(q), values(k), values(k), 128 ** -0.5, False)
+    assert_close(out, ref, torch.bfloat16, paged=False)

@@ -186,13 +186,13 @@ def test_no_early_reads_of_inline_mfma_results(tmp_path):
     subprocess.run(cmd, check=True, capture_output=True)
     text = out.read_text().splitlines()
     found = 0
-    for e in (32, 64, 128):
-        name = f"_ZN2ca21flash_bf16_p64_kernelILi{e}EEEvNS_11FlashParamsE:"
+    for e, split in ((e, b) for e in (32, 64, 128) for b in (0, 1)):
+        name = f"_ZN2ca21flash_bf16_p64_kernelILi{e}ELb{split}EEEvNS_11FlashParamsE:"
         start = next(i for i, x in enumerate(text) if x.startswith(name))
         end = next(i for i in range(start, len(text)) if text[i].startswith(".Lfunc_end"))
         body = text[start + 1:end]
         assert sum(1 for x in body if "v_mfma" in x) > 30
         report = hazards(body)
-        assert report == [], f"E={e}:\n" + "\n".join(report[:10])
+        assert report == [], f"E={e} split={split}:\n" + "\n".join(report[:10])
         found += 1
-    assert found == 3
+    assert found == 6
