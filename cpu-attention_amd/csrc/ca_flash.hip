@@ -1042,7 +1042,10 @@ struct FlashF32Cfg {
   static constexpr int LDS_BYTES = 2 * (LDS_K + LDS_V) * 4;
 };
 
-template <int E>
+// SPLIT: blockIdx.y is one of gridDim.y splits of the key range, each a run of
+// whole tiles; the block writes unnormalised (O, max, sum) partials of its rows
+// for the combine kernel instead of the output.
+template <int E, bool SPLIT>
 __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
   using C = FlashF32Cfg<E>;
   constexpr int BN = C::BN, KS = C::KS, VS = C::VS;
@@ -1059,10 +1062,28 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
   const float* vg = reinterpret_cast<const float*>(p.v) + bw.b * p.vs[0] + bw.h * p.vs[2];
 
   const int64_t row = bw.q0 + 32 * wv + li;
-  const int64_t kend_blk = p.causal ? min<int64_t>(S, bw.q0 + kBM + diag) : S;
-  const int nkt = kend_blk > 0 ? (int)cdiv(kend_blk, BN) : 0;
-  if (nkt == 0) {  // every row of the block sees no key: exactly 0
-    if (row < L) {
+  int64_t kbeg = 0, kend_blk = p.causal ? min<int64_t>(S, bw.q0 + kBM + diag) : S;
+  int sp = 0, splits = 1;
+  if constexpr (SPLIT) {
+    sp = blockIdx.y;
+    splits = gridDim.y;
+    const int64_t chunk = cdiv(cdiv(S, BN), splits) * BN;
+    kbeg = min<int64_t>(sp * chunk, max<int64_t>(kend_blk, 0));
+    kend_blk = min<int64_t>(kbeg + chunk, kend_blk);
+  }
+  // The partial slot of (row, split): O at part_acc[slot * E], (max, sum) at part_ml[2 * slot].
+  const int64_t slot = ((bw.b * p.heads + bw.h) * L + row) * splits + sp;
+  const int nkt = kend_blk > kbeg ? (int)cdiv(kend_blk - kbeg, BN) : 0;
+  if (nkt == 0) {  // every row of the block sees no key of this range: exactly 0
+    if (SPLIT && row < L) {
+      float* pa = p.part_acc + slot * E;
+#pragma unroll
+      for (int d = 0; d < E / 2; d += 4) *reinterpret_cast<f32x4*>(pa + (E / 2) * hf + d) = f32x4{0, 0, 0, 0};
+      if (hf == 0) {
+        p.part_ml[2 * slot] = -INFINITY;
+        p.part_ml[2 * slot + 1] = 0.f;
+      }
+    } else if (row < L) {
       float* og = reinterpret_cast<float*>(p.out) + ((bw.b * L + row) * p.heads + bw.h) * E;
 #pragma unroll
       for (int d = 0; d < E / 2; d += 4) *reinterpret_cast<f32x4*>(og + (E / 2) * hf + d) = f32x4{0, 0, 0, 0};
@@ -1095,7 +1116,7 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
     voff[i] = (int)((r * p.vs[1] + 4 * c4) * 4);
   }
   auto load_tile = [&](int t) {
-    const int64_t k0 = (int64_t)t * BN;
+    const int64_t k0 = kbeg + (int64_t)t * BN;
     const int64_t kbytes = ((S - 1 - k0) * p.ks[1] + E) * 4, vbytes = ((S - 1 - k0) * p.vs[1] + E) * 4;
     const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kg + k0 * p.ks[1], kbytes);
     const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vg + k0 * p.vs[1], vbytes);
@@ -1128,8 +1149,8 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
   __syncthreads();
   for (int t = 0; t < nkt; ++t) {
     const int buf = t & 1;
-    load_tile(t + 1);  // past the last tile: range-checked zeros, never used
-    const int64_t k0 = (int64_t)t * BN;
+    load_tile(t + 1);  // past the last tile: never used (range-checked zeros past S)
+    const int64_t k0 = kbeg + (int64_t)t * BN;
     if (k0 < kend_w) {
       const float* kb = Ks + buf * C::LDS_K;
       const float* vb = Vs + buf * C::LDS_V;
@@ -1182,6 +1203,22 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if constexpr (SPLIT) {
+    if (row < L) {
+      float* pa = p.part_acc + slot * E;
+#pragma unroll
+      for (int d = 0; d < E / 32; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(pa + 32 * d + 8 * g + 4 * hf) =
+              f32x4{oacc[d][4 * g], oacc[d][4 * g + 1], oacc[d][4 * g + 2], oacc[d][4 * g + 3]};
+      if (hf == 0) {
+        p.part_ml[2 * slot] = m_run;
+        p.part_ml[2 * slot + 1] = l_tot;
+      }
+    }
+    return;
+  }
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (row < L) {
     float* og = reinterpret_cast<float*>(p.out) + ((bw.b * L + row) * p.heads + bw.h) * E;
@@ -1221,14 +1258,16 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
   // Row and key positions are 32-bit inside the kernels.
   if (p.seq_q >= ((int64_t)1 << 30) || p.seq_k >= ((int64_t)1 << 30)) return CA_DECLINED;
   if (rows_route(p.seq_q, bf16 != 0)) return flash_rows_launch(p, E, bf16, stream);
+  // Split mode: one block per (batch, head, query block) and split of its keys,
+  // then the combine of each row's partials into the output.
+  const int64_t splits = tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, bf16 != 0);
+  if (splits > 1) {
+    const int64_t need = tiled_workspace_bytes(p.batch, p.seq_q, p.seq_k, p.heads, E, bf16 != 0);
+    if (p.part_acc == nullptr || p.part_ml == nullptr || p.workspace_bytes < need) return CA_DECLINED;
+  }
   if (bf16) {
     const int64_t nqb = cdiv(p.seq_q, FlashP64Cfg<128>::BM);
-    const int64_t splits = tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, true);
     if (splits > 1) {
-      // One block per (batch, head, query block) and split of its keys, then the
-      // combine of each row's partials into the output.
-      const int64_t need = tiled_workspace_bytes(p.batch, p.seq_q, p.seq_k, p.heads, E, true);
-      if (p.part_acc == nullptr || p.part_ml == nullptr || p.workspace_bytes < need) return CA_DECLINED;
       const int64_t nb = p.batch * p.heads * nqb;
       int st = CA_DECLINED;
       switch (E) {
@@ -1248,10 +1287,20 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
     }
   } else {
     const int64_t nb = p.batch * p.heads * cdiv(p.seq_q, kBM);
+    if (splits > 1) {
+      int st = CA_DECLINED;
+      switch (E) {
+        case 32: st = launch_lds(flash_f32_kernel<32, true>, nb, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream, splits); break;
+        case 64: st = launch_lds(flash_f32_kernel<64, true>, nb, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream, splits); break;
+        case 128: st = launch_lds(flash_f32_kernel<128, true>, nb, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream, splits); break;
+      }
+      if (st != CA_OK) return st;
+      return flash_combine_launch(p, E, bf16, splits, stream);
+    }
     switch (E) {
-      case 32: return launch_lds(flash_f32_kernel<32>, nb, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream);
-      case 64: return launch_lds(flash_f32_kernel<64>, nb, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream);
-      case 128: return launch_lds(flash_f32_kernel<128>, nb, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream);
+      case 32: return launch_lds(flash_f32_kernel<32, false>, nb, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream);
+      case 64: return launch_lds(flash_f32_kernel<64, false>, nb, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream);
+      case 128: return launch_lds(flash_f32_kernel<128, false>, nb, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream);
     }
   }
   return CA_DECLINED;

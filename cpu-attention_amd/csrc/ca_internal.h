@@ -75,24 +75,25 @@ constexpr int kRowsWaves = 8;                 // waves per block
 constexpr int64_t kRowsTargetBlocks = 256;    // blocks that keep every CU streaming
 constexpr int64_t kRowsMaxSplits = 64;
 
-// The bf16 tiled prefill splits each query block's keys over several blocks when
-// its query blocks (batch x heads x ceil(seq_q / 256)) leave the chip's CUs short
-// of blocks: about kTiledTargetBlocks blocks, at least kTiledMinTiles key tiles
-// of 64 per split, at most kTiledMaxSplits.  Such calls (few rows over long key
-// ranges) are bound by reading K and V; with one block per query block a block's
-// serial walk over every key tile is the whole call's time.  The decision does
-// not look at `causal`, so the workspace query need not know it.
+// The tiled prefill splits each query block's keys over several blocks when its
+// query blocks (batch x heads x ceil(seq_q / rows per block): 256 rows in bf16,
+// 128 in fp32) leave the chip's CUs short of blocks: about kTiledTargetBlocks
+// blocks, at least kTiledMinKeys keys per split, at most kTiledMaxSplits.  Such
+// calls (few rows over long key ranges) would otherwise leave most CUs idle,
+// with a block's serial walk over every key tile the whole call's time.  The
+// decision does not look at `causal`, so the workspace query need not know it.
 constexpr int64_t kTiledTargetBlocks = 256;
-constexpr int64_t kTiledMinTiles = 4;
+constexpr int64_t kTiledMinKeys = 256;
 constexpr int64_t kTiledMaxSplits = 64;
 __host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads,
                                                 bool bf16) {
-  if (!bf16 || rows_route(seq_q, bf16)) return 1;
-  const int64_t items = batch * heads * ((seq_q + 255) / 256);
+  if (rows_route(seq_q, bf16)) return 1;
+  const int64_t bm = bf16 ? 256 : 128;
+  const int64_t items = batch * heads * ((seq_q + bm - 1) / bm);
   if (items <= 0 || items >= kTiledTargetBlocks) return 1;
   int64_t s = (kTiledTargetBlocks + items - 1) / items;
-  const int64_t by_tiles = (seq_k + 63) / 64 / kTiledMinTiles;
-  s = s < by_tiles ? s : by_tiles;
+  const int64_t by_keys = (seq_k + 63) / 64 / (kTiledMinKeys / 64);
+  s = s < by_keys ? s : by_keys;
   s = s < kTiledMaxSplits ? s : kTiledMaxSplits;
   return s < 2 ? 1 : s;
 }

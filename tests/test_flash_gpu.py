@@ -218,32 +218,34 @@ def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq):
 
 
 # Calls whose query blocks leave most CUs idle split each query block's keys over
-# several blocks (split mode of the bf16 tiled kernel): (batch, seq_q, seq_k, heads).
+# several blocks (split mode of the tiled kernels): (batch, seq_q, seq_k, heads).
 SPLIT_SHAPES = [(1, 64, 4096, 32), (1, 17, 2100, 8), (2, 300, 1500, 4), (1, 600, 4000, 3)]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("shape", SPLIT_SHAPES)
-def test_split_keys(cuda, d, causal, shape):
+def test_split_keys(cuda, d, causal, shape, dtype):
     """Few query rows over long key ranges, so the keys of each query block are
     split over several blocks and the row partials merged by the combine kernel:
     unequal lengths, partial last tiles and query blocks, causal ranges that end
     inside a split and splits past a query block's last key."""
     b, sq, sk, h = shape
-    run(b, sq, sk, h, d, torch.bfloat16, causal, 31 + sq, cuda)
+    run(b, sq, sk, h, d, dtype, causal, 31 + sq, cuda)
 
 
-def test_split_keys_rows_without_keys(cuda):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_split_keys_rows_without_keys(cuda, dtype):
     """Causal with more query rows than keys: the first rows see no key (exactly 0)
     in every split."""
     g = torch.Generator().manual_seed(32)
-    q = torch.randn(1, 700, 4, 64, generator=g).bfloat16().to(cuda)
-    k, v = (torch.randn(1, 600, 4, 64, generator=g).bfloat16().to(cuda) for _ in range(2))
+    q = torch.randn(1, 700, 4, 64, generator=g).to(dtype).to(cuda)
+    k, v = (torch.randn(1, 600, 4, 64, generator=g).to(dtype).to(cuda) for _ in range(2))
     out = flash_attn_func(q, k, v, causal=True)
     assert torch.count_nonzero(out[:, :100]) == 0
     ref = attention(values(q), values(k), values(v), 64 ** -0.5, True)
-    assert_close(out, ref, torch.bfloat16, paged=False)
+    assert_close(out, ref, dtype, paged=False)
 
 
 @pytest.mark.parametrize("d", [64, 128])
@@ -264,16 +266,17 @@ def test_split_keys_safe_pass(cuda, d):
         assert_close(out, ref, torch.bfloat16, paged=False)
 
 
-def test_split_keys_module_asks_for_workspace(cuda):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_split_keys_module_asks_for_workspace(cuda, dtype):
     """The native module's flash returns the workspace bytes a split call needs when
     it gets less (the reference's grow-and-retry, flash_attn_interface.py:186-193)."""
     from cpu_attention import _kernel as K
     mod = K.module()
-    q = torch.randn(1, 64, 32, 128, device=cuda).bfloat16()
-    k = torch.randn(1, 4096, 32, 128, device=cuda).bfloat16()
+    q = torch.randn(1, 64, 32, 128, device=cuda).to(dtype)
+    k = torch.randn(1, 4096, 32, 128, device=cuda).to(dtype)
     need = mod.flash(K.runtime(), q, k, k, None, False, None, 0)
     assert isinstance(need, int) and need == 32 * 64 * 8 * 130 * 4
     ws = torch.empty(need, dtype=torch.uint8, device=cuda)
     out = mod.flash(K.runtime(), q, k, k, None, False, ws.data_ptr(), need)
     ref = attention(values(q), values(k), values(k), 128 ** -0.5, False)
-    assert_close(out, ref, torch.bfloat16, paged=False)
+    assert_close(out, ref, dtype, paged=False)
