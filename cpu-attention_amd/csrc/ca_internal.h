@@ -78,7 +78,8 @@ constexpr int64_t kRowsMaxSplits = 64;
 // The tiled prefill splits each query block's keys over several blocks when its
 // query blocks (batch x heads x ceil(seq_q / rows per block): 256 rows in bf16,
 // 128 in fp32) leave the chip's CUs short of blocks: about kTiledTargetBlocks
-// blocks, at least kTiledMinKeys keys per split, at most kTiledMaxSplits.  Such
+// blocks (twice that in fp32, whose kernel keeps two blocks on each CU), at least
+// kTiledMinKeys keys per split, at most kTiledMaxSplits.  Such
 // calls (few rows over long key ranges) would otherwise leave most CUs idle,
 // with a block's serial walk over every key tile the whole call's time.  The
 // decision does not look at `causal`, so the workspace query need not know it.
@@ -90,8 +91,9 @@ __host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, in
   if (rows_route(seq_q, bf16)) return 1;
   const int64_t bm = bf16 ? 256 : 128;
   const int64_t items = batch * heads * ((seq_q + bm - 1) / bm);
-  if (items <= 0 || items >= kTiledTargetBlocks) return 1;
-  int64_t s = (kTiledTargetBlocks + items - 1) / items;
+  const int64_t target = bf16 ? kTiledTargetBlocks : 2 * kTiledTargetBlocks;
+  if (items <= 0 || items >= target) return 1;
+  int64_t s = (target + items - 1) / items;
   const int64_t by_keys = (seq_k + 63) / 64 / (kTiledMinKeys / 64);
   s = s < by_keys ? s : by_keys;
   s = s < kTiledMaxSplits ? s : kTiledMaxSplits;

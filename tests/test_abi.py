@@ -153,14 +153,15 @@ def test_flash_workspace_for_few_rows(dtype, d, chunk):
 
 def tiled(b, sq, sk, h, d, dtype):
     """The tiled prefill's split mode: when its query blocks (b * h * ceil(sq /
-    rows per block): 256 in bf16, 128 in fp32) number fewer than 256, each one's
-    keys are split over about 256 / blocks blocks, at least 256 keys each (whole
-    64-key units) and at most 64 splits, which needs (E + 2) floats per (batch,
-    head, row, split)."""
+    rows per block): 256 in bf16, 128 in fp32) number fewer than a target (256 in
+    bf16, 512 in fp32), each one's keys are split over about target / blocks
+    blocks, at least 256 keys each (whole 64-key units) and at most 64 splits,
+    which needs (E + 2) floats per (batch, head, row, split)."""
     blocks = b * h * -(-sq // (256 if dtype == 1 else 128))
-    if blocks >= 256:
+    target = 256 if dtype == 1 else 512
+    if blocks >= target:
         return 0
-    splits = min(-(-256 // blocks), -(-sk // 64) // 4, 64)
+    splits = min(-(-target // blocks), -(-sk // 64) // 4, 64)
     return 0 if splits < 2 else b * h * sq * splits * (d + 2) * 4
 
 
@@ -168,17 +169,18 @@ def tiled(b, sq, sk, h, d, dtype):
 def test_flash_workspace_for_split_keys(d):
     lib = K.load_library()
     for b, sq, sk, h in ((1, 64, 4096, 32), (1, 17, 2100, 8), (2, 300, 1500, 4), (4, 4096, 4096, 32),
-                         (1, 128, 128, 16), (1, 600, 255, 3), (1, 5, 100000, 1), (1, 200, 4096, 128)):
+                         (1, 128, 128, 16), (1, 600, 255, 3), (1, 5, 100000, 1), (1, 100, 4096, 300)):
         assert lib.ca_flash_workspace_bytes(b, sq, sk, h, d, 1) == tiled(b, sq, sk, h, d, 1)
         if sq > 16:  # fp32 past the few-rows route
             assert lib.ca_flash_workspace_bytes(b, sq, sk, h, d, 0) == tiled(b, sq, sk, h, d, 0)
+    assert lib.ca_flash_workspace_bytes(1, 64, 4096, 32, d, 1) == 32 * 64 * 8 * (d + 2) * 4  # 8 splits
+    assert lib.ca_flash_workspace_bytes(1, 64, 4096, 32, d, 0) == 32 * 64 * 16 * (d + 2) * 4  # 16 splits
     for dtype in (0, 1):
-        assert lib.ca_flash_workspace_bytes(1, 64, 4096, 32, d, dtype) == 32 * 64 * 8 * (d + 2) * 4  # 8 splits
         assert lib.ca_flash_workspace_bytes(4, 4096, 4096, 32, d, dtype) == 0  # cfg4: >= 2048 query blocks
         assert lib.ca_flash_workspace_bytes(1, 128, 128, 16, d, dtype) == 0  # cfg1: 128 keys
-    # 200 rows are one bf16 block but two fp32 blocks: 128 heads fill the chip in fp32 only
-    assert lib.ca_flash_workspace_bytes(1, 200, 4096, 128, d, 1) == 200 * 128 * 2 * (d + 2) * 4
-    assert lib.ca_flash_workspace_bytes(1, 200, 4096, 128, d, 0) == 0
+    # 300 query blocks fill the chip in bf16 (one block per CU) but not in fp32 (two)
+    assert lib.ca_flash_workspace_bytes(1, 100, 4096, 300, d, 1) == 0
+    assert lib.ca_flash_workspace_bytes(1, 100, 4096, 300, d, 0) == 100 * 300 * 2 * (d + 2) * 4
 
 
 def test_missing_library_is_a_loud_error(monkeypatch):

@@ -275,7 +275,8 @@ def test_split_keys_module_asks_for_workspace(cuda, dtype):
     q = torch.randn(1, 64, 32, 128, device=cuda).to(dtype)
     k = torch.randn(1, 4096, 32, 128, device=cuda).to(dtype)
     need = mod.flash(K.runtime(), q, k, k, None, False, None, 0)
-    assert isinstance(need, int) and need == 32 * 64 * 8 * 130 * 4
+    splits = 8 if dtype == torch.bfloat16 else 16  # 32 query blocks against 256 / 512 target blocks
+    assert isinstance(need, int) and need == 32 * 64 * splits * 130 * 4
     ws = torch.empty(need, dtype=torch.uint8, device=cuda)
     out = mod.flash(K.runtime(), q, k, k, None, False, ws.data_ptr(), need)
     ref = attention(values(q), values(k), values(k), 128 ** -0.5, False)
