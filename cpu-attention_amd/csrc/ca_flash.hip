@@ -106,9 +106,18 @@ struct PairWork {
   int n;
 };
 
+// Causal calls pair query blocks (qb, nqb-1-qb), so that every block has the
+// same work, unless the unpaired query blocks number few enough to all run at
+// once (one block per CU): then pairs would leave CUs idle.
+constexpr int64_t kPairMinBlocks = 256;  // the chip's CUs
+__host__ __device__ inline bool pair_blocks(const FlashParams& p, int64_t nqb) {
+  return p.causal && p.batch * p.heads * nqb > kPairMinBlocks;
+}
+
 __device__ __forceinline__ PairWork pair_work(const FlashParams& p, int bm) {
   const int64_t nqb = cdiv(p.seq_q, bm);
-  const int64_t per = p.causal ? (nqb + 1) / 2 : nqb;
+  const bool pair = pair_blocks(p, nqb);
+  const int64_t per = pair ? (nqb + 1) / 2 : nqb;
   const int64_t lg = xcd_remap(blockIdx.x, p.batch * p.heads * per);
   const int64_t bh = lg / per, j = lg - bh * per;
   PairWork w;
@@ -116,7 +125,7 @@ __device__ __forceinline__ PairWork pair_work(const FlashParams& p, int bm) {
   w.h = bh - w.b * p.heads;
   w.qb0 = p.causal ? nqb - 1 - j : j;
   w.qb1 = j;
-  w.n = (p.causal && w.qb0 != j) ? 2 : 1;
+  w.n = (pair && w.qb0 != j) ? 2 : 1;
   return w;
 }
 
@@ -1279,7 +1288,7 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
       return flash_combine_launch(p, E, bf16, splits, stream);
     }
     // One block per (batch, head) and query-block pair (causal) or query block.
-    const int64_t nb = p.batch * p.heads * (p.causal ? (nqb + 1) / 2 : nqb);
+    const int64_t nb = p.batch * p.heads * (pair_blocks(p, nqb) ? (nqb + 1) / 2 : nqb);
     switch (E) {
       case 32: return launch_lds(flash_bf16_p64_kernel<32, false>, nb, 64 * FlashP64Cfg<32>::NW, FlashP64Cfg<32>::LDS_BYTES, p, stream);
       case 64: return launch_lds(flash_bf16_p64_kernel<64, false>, nb, 64 * FlashP64Cfg<64>::NW, FlashP64Cfg<64>::LDS_BYTES, p, stream);

@@ -177,7 +177,7 @@ def test_safe_pass_for_one_pass_of_a_causal_pair(cuda, d, bad_pass):
     holds rows whose logits outgrow the fast walk's fixed max; the block redoes
     exactly those after both passes and keeps the other pass's fast results."""
     g = torch.Generator().manual_seed(12 + bad_pass)
-    b, L, h = 1, 512, 2
+    b, L, h = 1, 512, 130  # 260 query blocks: paired
     q = torch.randn(b, L, h, d, generator=g) * 0.5 + 1.0
     k = torch.randn(b, L, h, d, generator=g) * 0.5
     # a key whose logits sit about 100 log2 units above the first tile's (past the
@@ -191,21 +191,26 @@ def test_safe_pass_for_one_pass_of_a_causal_pair(cuda, d, bad_pass):
     q, k = q.bfloat16().to(cuda), k.bfloat16().to(cuda)
     v = torch.randn(b, L, h, d, generator=g).bfloat16().to(cuda)
     out = flash_attn_func(q, k, v, causal=True)
-    ref = attention(values(q), values(k), values(v), d ** -0.5, True)
-    assert_close(out, ref, torch.bfloat16, paged=False)
+    for hh in (0, h - 1):
+        sel = slice(hh, hh + 1)
+        ref = attention(values(q[:, :, sel]), values(k[:, :, sel]), values(v[:, :, sel]), d ** -0.5, True)
+        assert_close(out[:, :, sel], ref, torch.bfloat16, paged=False)
 
 
 @pytest.mark.parametrize("d", [64, 128])
-@pytest.mark.parametrize("causal,sq", [(True, 1536), (False, 600)])
-def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq):
+@pytest.mark.parametrize("causal,sq,h", [(True, 1536, 2), (False, 600, 2), (True, 1536, 44), (False, 600, 86)])
+def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq, h):
     """Key 100 sits about 100 log2 units above every row's first-tile max, so every
     wave whose rows all see it fails the fast walk's headroom from tile 1 on, and
     whole blocks redo their rows in the safe pass.  Causal, 1536 rows: the pair
     (rows 1280-1535, rows 0-255) fails all of its first pass and part of its second
     (whose first wave never sees key 100).  Non-causal, 600 rows over 1536 keys:
-    every full block fails; the last block's waves past row 599 do not."""
+    every full block fails; the last block's waves past row 599 do not.  With 2
+    heads the query blocks are few, so their keys are split over blocks (the safe
+    pass writes partials); with 44 or 86 heads they fill the chip (pairs when
+    causal, one block per query block otherwise)."""
     g = torch.Generator().manual_seed(13)
-    b, h = 1, 2
+    b = 1
     sk = 1536
     q = torch.randn(b, sq, h, d, generator=g) * 0.5 + 1.0
     k = torch.randn(b, sk, h, d, generator=g) * 0.5
@@ -213,8 +218,30 @@ def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq):
     q, k = q.bfloat16().to(cuda), k.bfloat16().to(cuda)
     v = torch.randn(b, sk, h, d, generator=g).bfloat16().to(cuda)
     out = flash_attn_func(q, k, v, causal=causal)
-    ref = attention(values(q), values(k), values(v), d ** -0.5, causal)
-    assert_close(out, ref, torch.bfloat16, paged=False)
+    for hh in (0, h - 1):
+        sel = slice(hh, hh + 1)
+        ref = attention(values(q[:, :, sel]), values(k[:, :, sel]), values(v[:, :, sel]), d ** -0.5, causal)
+        assert_close(out[:, :, sel], ref, torch.bfloat16, paged=False)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("b,sq,sk,h", [(1, 600, 600, 130), (1, 400, 400, 8), (1, 2048, 2048, 32),
+                                       (2, 700, 1200, 48)])
+def test_causal_block_schedules(cuda, d, b, sq, sk, h):
+    """The bf16 kernel's causal block schedules, each checked on a few heads:
+    query-block pairs (qb, nqb-1-qb) in one block when there are more than 256
+    query blocks (1 x 130 x 3 = 390: two pairs and one lone block per head; 2 x 48
+    x 3 = 288 with more keys than rows), and one block per query block when they
+    all fit the chip at once (16 blocks over 400 keys, too few keys to split; 256
+    blocks at L = S = 2048)."""
+    g = torch.Generator().manual_seed(40 + h)
+    q = torch.randn(b, sq, h, d, generator=g).bfloat16().to(cuda)
+    k, v = (torch.randn(b, sk, h, d, generator=g).bfloat16().to(cuda) for _ in range(2))
+    out = flash_attn_func(q, k, v, causal=True)
+    for hh in sorted({0, h // 2, h - 1}):
+        sel = slice(hh, hh + 1)
+        ref = attention(values(q[:, :, sel]), values(k[:, :, sel]), values(v[:, :, sel]), d ** -0.5, True)
+        assert_close(out[:, :, sel], ref, torch.bfloat16, paged=False)
 
 
 # Calls whose query blocks leave most CUs idle split each query block's keys over
