@@ -732,7 +732,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                          "frac_cold": round(flop / (pcmed * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                         "traffic": traffic_bytes("prefill"), "kernel": "flash_bf16_p64_kernel<128>",
+                         "traffic": traffic_bytes("prefill"), "kernel": "flash_bf16_p64_kernel<128, false>",
                          "algorithmic_flop": flop},
         }
         del qkv, q, k, v
