@@ -109,14 +109,15 @@ struct PairWork {
 // Causal calls pair query blocks (qb, nqb-1-qb), so that every block has the
 // same work, unless the unpaired query blocks number few enough to all run at
 // once (one block per CU): then pairs would leave CUs idle.
+// The fp32 kernel keeps two blocks on each CU, so it pairs past twice as many.
 constexpr int64_t kPairMinBlocks = 256;  // the chip's CUs
-__host__ __device__ inline bool pair_blocks(const FlashParams& p, int64_t nqb) {
-  return p.causal && p.batch * p.heads * nqb > kPairMinBlocks;
+__host__ __device__ inline bool pair_blocks(const FlashParams& p, int64_t nqb, int64_t min_blocks) {
+  return p.causal && p.batch * p.heads * nqb > min_blocks;
 }
 
-__device__ __forceinline__ PairWork pair_work(const FlashParams& p, int bm) {
+__device__ __forceinline__ PairWork pair_work(const FlashParams& p, int bm, int64_t min_blocks) {
   const int64_t nqb = cdiv(p.seq_q, bm);
-  const bool pair = pair_blocks(p, nqb);
+  const bool pair = pair_blocks(p, nqb, min_blocks);
   const int64_t per = pair ? (nqb + 1) / 2 : nqb;
   const int64_t lg = xcd_remap(blockIdx.x, p.batch * p.heads * per);
   const int64_t bh = lg / per, j = lg - bh * per;
@@ -894,7 +895,7 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
     sp = blockIdx.y;
     splits = gridDim.y;
   } else {
-    pw = pair_work(p, BM);
+    pw = pair_work(p, BM, kPairMinBlocks);
   }
   // Positions and token strides fit 32 bits (the launcher declines otherwise).
   Bf16Pass a;
@@ -1054,8 +1055,13 @@ struct FlashF32Cfg {
 // SPLIT: blockIdx.y is one of gridDim.y splits of the key range, each a run of
 // whole tiles; the block writes unnormalised (O, max, sum) partials of its rows
 // for the combine kernel instead of the output.
-template <int E, bool SPLIT>
+//
+// PAIR (causal calls of more than 512 query blocks): the block runs the pair
+// (qb, nqb-1-qb) one pass after the other, so every block does the same work;
+// otherwise one query block, the most expensive causal blocks first.
+template <int E, bool SPLIT, bool PAIR>
 __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
+  static_assert(!(SPLIT && PAIR), "split calls are not paired");
   using C = FlashF32Cfg<E>;
   constexpr int BN = C::BN, KS = C::KS, VS = C::VS;
   extern __shared__ __attribute__((aligned(16))) float smemf[];
@@ -1064,7 +1070,12 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int li = lane & 31, hf = lane >> 5;
-  const BlockWork bw = block_work(p);
+  PairWork pw{};
+  if constexpr (PAIR) pw = pair_work(p, kBM, 2 * kPairMinBlocks);
+#pragma unroll 1
+  for (int pass = 0; pass < (PAIR ? pw.n : 1); ++pass) {
+  if (PAIR && pass > 0) __syncthreads();  // the first pass's tile buffers are free again
+  const BlockWork bw = PAIR ? BlockWork{pw.b, pw.h, (pass ? pw.qb1 : pw.qb0) * kBM} : block_work(p);
   const int64_t L = p.seq_q, S = p.seq_k, diag = S - L;
   const float* qg = reinterpret_cast<const float*>(p.q) + bw.b * p.qs[0] + bw.h * p.qs[2];
   const float* kg = reinterpret_cast<const float*>(p.k) + bw.b * p.ks[0] + bw.h * p.ks[2];
@@ -1097,7 +1108,7 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
 #pragma unroll
       for (int d = 0; d < E / 2; d += 4) *reinterpret_cast<f32x4*>(og + (E / 2) * hf + d) = f32x4{0, 0, 0, 0};
     }
-    return;
+    continue;
   }
 
   // Q: lane (query li, half hf) holds dims 4t+2hf and 4t+2hf+1.
@@ -1226,7 +1237,7 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
         p.part_ml[2 * slot + 1] = l_tot;
       }
     }
-    return;
+    continue;
   }
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (row < L) {
@@ -1239,6 +1250,7 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
             f32x4{oacc[d][4 * g] * inv, oacc[d][4 * g + 1] * inv, oacc[d][4 * g + 2] * inv,
                   oacc[d][4 * g + 3] * inv};
   }
+  }  // passes
 }
 
 template <typename K>
@@ -1288,28 +1300,38 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
       return flash_combine_launch(p, E, bf16, splits, stream);
     }
     // One block per (batch, head) and query-block pair (causal) or query block.
-    const int64_t nb = p.batch * p.heads * (pair_blocks(p, nqb) ? (nqb + 1) / 2 : nqb);
+    const int64_t nb = p.batch * p.heads * (pair_blocks(p, nqb, kPairMinBlocks) ? (nqb + 1) / 2 : nqb);
     switch (E) {
       case 32: return launch_lds(flash_bf16_p64_kernel<32, false>, nb, 64 * FlashP64Cfg<32>::NW, FlashP64Cfg<32>::LDS_BYTES, p, stream);
       case 64: return launch_lds(flash_bf16_p64_kernel<64, false>, nb, 64 * FlashP64Cfg<64>::NW, FlashP64Cfg<64>::LDS_BYTES, p, stream);
       case 128: return launch_lds(flash_bf16_p64_kernel<128, false>, nb, 64 * FlashP64Cfg<128>::NW, FlashP64Cfg<128>::LDS_BYTES, p, stream);
     }
   } else {
-    const int64_t nb = p.batch * p.heads * cdiv(p.seq_q, kBM);
+    const int64_t nqb = cdiv(p.seq_q, kBM);
+    const int64_t nb = p.batch * p.heads * nqb;
     if (splits > 1) {
       int st = CA_DECLINED;
       switch (E) {
-        case 32: st = launch_lds(flash_f32_kernel<32, true>, nb, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream, splits); break;
-        case 64: st = launch_lds(flash_f32_kernel<64, true>, nb, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream, splits); break;
-        case 128: st = launch_lds(flash_f32_kernel<128, true>, nb, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream, splits); break;
+        case 32: st = launch_lds(flash_f32_kernel<32, true, false>, nb, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream, splits); break;
+        case 64: st = launch_lds(flash_f32_kernel<64, true, false>, nb, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream, splits); break;
+        case 128: st = launch_lds(flash_f32_kernel<128, true, false>, nb, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream, splits); break;
       }
       if (st != CA_OK) return st;
       return flash_combine_launch(p, E, bf16, splits, stream);
     }
+    if (pair_blocks(p, nqb, 2 * kPairMinBlocks)) {
+      const int64_t nbp = p.batch * p.heads * ((nqb + 1) / 2);
+      switch (E) {
+        case 32: return launch_lds(flash_f32_kernel<32, false, true>, nbp, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream);
+        case 64: return launch_lds(flash_f32_kernel<64, false, true>, nbp, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream);
+        case 128: return launch_lds(flash_f32_kernel<128, false, true>, nbp, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream);
+      }
+      return CA_DECLINED;
+    }
     switch (E) {
-      case 32: return launch_lds(flash_f32_kernel<32, false>, nb, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream);
-      case 64: return launch_lds(flash_f32_kernel<64, false>, nb, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream);
-      case 128: return launch_lds(flash_f32_kernel<128, false>, nb, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream);
+      case 32: return launch_lds(flash_f32_kernel<32, false, false>, nb, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream);
+      case 64: return launch_lds(flash_f32_kernel<64, false, false>, nb, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream);
+      case 128: return launch_lds(flash_f32_kernel<128, false, false>, nb, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream);
     }
   }
   return CA_DECLINED;
