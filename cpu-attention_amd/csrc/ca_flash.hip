@@ -108,16 +108,23 @@ struct PairWork {
 
 // Causal calls pair query blocks (qb, nqb-1-qb), so that every block has the
 // same work, unless the unpaired query blocks number few enough to all run at
-// once (one block per CU): then pairs would leave CUs idle.
-// The fp32 kernel keeps two blocks on each CU, so it pairs past twice as many.
+// once: then pairs would leave CUs idle.  bf16 (256-row blocks, one per CU):
+// pairs past 256 query blocks.  fp32 (128-row blocks, two per CU; below 512 the
+// split mode runs instead): pairs from 1024, or from 512 when the causal
+// triangle is most of the work (fewer than twice as many keys as rows); with
+// more keys the blocks' work is nearly even, and 512 blocks as 256 pairs would
+// leave each CU one block instead of two.
 constexpr int64_t kPairMinBlocks = 256;  // the chip's CUs
-__host__ __device__ inline bool pair_blocks(const FlashParams& p, int64_t nqb, int64_t min_blocks) {
-  return p.causal && p.batch * p.heads * nqb > min_blocks;
+__host__ __device__ inline bool pair_blocks(const FlashParams& p, int64_t nqb, bool bf16) {
+  const int64_t items = p.batch * p.heads * nqb;
+  if (!p.causal) return false;
+  if (bf16) return items > kPairMinBlocks;
+  return items >= 4 * kPairMinBlocks || (items >= 2 * kPairMinBlocks && p.seq_k < 2 * p.seq_q);
 }
 
-__device__ __forceinline__ PairWork pair_work(const FlashParams& p, int bm, int64_t min_blocks) {
+__device__ __forceinline__ PairWork pair_work(const FlashParams& p, int bm, bool bf16) {
   const int64_t nqb = cdiv(p.seq_q, bm);
-  const bool pair = pair_blocks(p, nqb, min_blocks);
+  const bool pair = pair_blocks(p, nqb, bf16);
   const int64_t per = pair ? (nqb + 1) / 2 : nqb;
   const int64_t lg = xcd_remap(blockIdx.x, p.batch * p.heads * per);
   const int64_t bh = lg / per, j = lg - bh * per;
@@ -895,7 +902,7 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
     sp = blockIdx.y;
     splits = gridDim.y;
   } else {
-    pw = pair_work(p, BM, kPairMinBlocks);
+    pw = pair_work(p, BM, true);
   }
   // Positions and token strides fit 32 bits (the launcher declines otherwise).
   Bf16Pass a;
@@ -1056,7 +1063,7 @@ struct FlashF32Cfg {
 // whole tiles; the block writes unnormalised (O, max, sum) partials of its rows
 // for the combine kernel instead of the output.
 //
-// PAIR (causal calls of more than 512 query blocks): the block runs the pair
+// PAIR (causal calls of many query blocks, pair_blocks()): the block runs the pair
 // (qb, nqb-1-qb) one pass after the other, so every block does the same work;
 // otherwise one query block, the most expensive causal blocks first.
 template <int E, bool SPLIT, bool PAIR>
@@ -1071,7 +1078,7 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int li = lane & 31, hf = lane >> 5;
   PairWork pw{};
-  if constexpr (PAIR) pw = pair_work(p, kBM, 2 * kPairMinBlocks);
+  if constexpr (PAIR) pw = pair_work(p, kBM, false);
 #pragma unroll 1
   for (int pass = 0; pass < (PAIR ? pw.n : 1); ++pass) {
   if (PAIR && pass > 0) __syncthreads();  // the first pass's tile buffers are free again
@@ -1300,7 +1307,7 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
       return flash_combine_launch(p, E, bf16, splits, stream);
     }
     // One block per (batch, head) and query-block pair (causal) or query block.
-    const int64_t nb = p.batch * p.heads * (pair_blocks(p, nqb, kPairMinBlocks) ? (nqb + 1) / 2 : nqb);
+    const int64_t nb = p.batch * p.heads * (pair_blocks(p, nqb, true) ? (nqb + 1) / 2 : nqb);
     switch (E) {
       case 32: return launch_lds(flash_bf16_p64_kernel<32, false>, nb, 64 * FlashP64Cfg<32>::NW, FlashP64Cfg<32>::LDS_BYTES, p, stream);
       case 64: return launch_lds(flash_bf16_p64_kernel<64, false>, nb, 64 * FlashP64Cfg<64>::NW, FlashP64Cfg<64>::LDS_BYTES, p, stream);
@@ -1319,7 +1326,7 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
       if (st != CA_OK) return st;
       return flash_combine_launch(p, E, bf16, splits, stream);
     }
-    if (pair_blocks(p, nqb, 2 * kPairMinBlocks)) {
+    if (pair_blocks(p, nqb, false)) {
       const int64_t nbp = p.batch * p.heads * ((nqb + 1) / 2);
       switch (E) {
         case 32: return launch_lds(flash_f32_kernel<32, false, true>, nbp, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream);

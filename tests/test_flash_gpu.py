@@ -227,16 +227,17 @@ def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq, h):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("b,sq,sk,h", [(1, 600, 600, 130), (1, 400, 400, 8), (1, 2048, 2048, 32),
-                                       (2, 700, 1200, 48)])
+                                       (2, 700, 1200, 48), (1, 2048, 4096, 32)])
 def test_causal_block_schedules(cuda, d, b, sq, sk, h, dtype):
     """The causal block schedules, each checked on a few heads: query-block pairs
-    (qb, nqb-1-qb) in one block when there are more query blocks than the chip
-    holds at once (bf16: 256 rows per query block, more than 256 of them; fp32: 128
-    rows, more than 512), else one block per query block.  bf16: 1 x 130 x 3 = 390
-    (two pairs and one lone block per head) and 2 x 48 x 3 = 288 (more keys than
-    rows) pair; 16 blocks over 400 keys (too few keys to split) and 256 blocks at
-    L = S = 2048 do not.  fp32: 650 and 576 query blocks pair (an odd and an even
-    count per head); 32 and 512 do not."""
+    (qb, nqb-1-qb) in one block when unpaired blocks would leave the chip
+    unevenly loaded, else one block per query block.  bf16 (256 rows per query
+    block) pairs past 256: 1 x 130 x 3 = 390 (two pairs and one lone block per
+    head) and 2 x 48 x 3 = 288 (more keys than rows) pair; 16 blocks over 400 keys
+    (too few keys to split) and 256 at L = 2048 do not.  fp32 (128 rows) pairs
+    from 1024, or from 512 with fewer than twice as many keys as rows: 650, 576
+    and 512 at L = S = 2048 pair (odd and even counts per head); 32, and 512 over
+    4096 keys, do not."""
     g = torch.Generator().manual_seed(40 + h)
     q = torch.randn(b, sq, h, d, generator=g).to(dtype).to(cuda)
     k, v = (torch.randn(b, sk, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))
