@@ -1288,9 +1288,9 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
   if (rows_route(p.seq_q, bf16 != 0)) return flash_rows_launch(p, E, bf16, stream);
   // Split mode: one block per (batch, head, query block) and split of its keys,
   // then the combine of each row's partials into the output.
-  const int64_t splits = tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, bf16 != 0);
+  const int64_t splits = tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, bf16 != 0, p.causal != 0);
   if (splits > 1) {
-    const int64_t need = tiled_workspace_bytes(p.batch, p.seq_q, p.seq_k, p.heads, E, bf16 != 0);
+    const int64_t need = tiled_workspace_bytes(p.batch, p.seq_q, p.seq_k, p.heads, E, bf16 != 0, p.causal != 0);
     if (p.part_acc == nullptr || p.part_ml == nullptr || p.workspace_bytes < need) return CA_DECLINED;
   }
   if (bf16) {
