@@ -161,8 +161,10 @@ int ca_decode_noalloc(const ca_decode_args* args, void* stream);
  * dtype.  Calls whose keys are split over several blocks leave partials in the
  * workspace: few-row calls (seq_q <= 4 bf16, <= 16 fp32), and calls with fewer
  * than 256 query blocks of 256 rows (bf16) or 512 of 128 rows (fp32) over long
- * key ranges.  Pass at least the bytes ca_flash_workspace_bytes() asks for (0
- * means none is needed; a shorter workspace declines the call).  The
+ * key ranges (bf16 causal calls only with at least twice as many keys as rows).
+ * Pass at least the bytes ca_flash_workspace_bytes() asks for (0 means none is
+ * needed; it answers for non-causal calls, which split at least as much; a
+ * shorter workspace declines the call).  The
  * reference's entry grows its workspace on request the same way
  * (flash_attn_interface.py:186-193). */
 typedef struct ca_flash_args {
