@@ -249,6 +249,23 @@ def test_causal_block_schedules(cuda, d, b, sq, sk, h, dtype):
         assert_close(out[:, :, sel], ref, dtype, paged=False)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_causal_pairs_with_rows_without_keys(cuda, dtype):
+    """Causal pairs whose low query blocks see no key: 2304 rows over 1024 keys, 32
+    heads (288 bf16 / 576 fp32 query blocks, both paired).  Rows below 1280 are
+    exactly 0, written by the passes that have no key tile."""
+    g = torch.Generator().manual_seed(50)
+    b, sq, sk, h, d = 1, 2304, 1024, 32, 64
+    q = torch.randn(b, sq, h, d, generator=g).to(dtype).to(cuda)
+    k, v = (torch.randn(b, sk, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))
+    out = flash_attn_func(q, k, v, causal=True)
+    assert torch.count_nonzero(out[:, :sq - sk]) == 0
+    for hh in (0, 17, 31):
+        sel = slice(hh, hh + 1)
+        ref = attention(values(q[:, :, sel]), values(k[:, :, sel]), values(v[:, :, sel]), d ** -0.5, True)
+        assert_close(out[:, :, sel], ref, dtype, paged=False)
+
+
 # Calls whose query blocks leave most CUs idle split each query block's keys over
 # several blocks (split mode of the tiled kernels): (batch, seq_q, seq_k, heads).
 SPLIT_SHAPES = [(1, 64, 4096, 32), (1, 17, 2100, 8), (2, 300, 1500, 4), (1, 600, 4000, 3)]
