@@ -1285,7 +1285,7 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
     return CA_DECLINED;
   // Row and key positions are 32-bit inside the kernels.
   if (p.seq_q >= ((int64_t)1 << 30) || p.seq_k >= ((int64_t)1 << 30)) return CA_DECLINED;
-  if (rows_route(p.seq_q, bf16 != 0)) return flash_rows_launch(p, E, bf16, stream);
+  if (rows_route(p.batch, p.seq_q, p.heads, bf16 != 0)) return flash_rows_launch(p, E, bf16, stream);
   // Split mode: one block per (batch, head, query block) and split of its keys,
   // then the combine of each row's partials into the output.
   const int64_t splits = tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, bf16 != 0, p.causal != 0);

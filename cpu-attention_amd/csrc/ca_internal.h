@@ -66,11 +66,18 @@ struct FlashParams {
 };
 
 // Calls with few query rows take the few-rows route (ca_rows.hip): up to 4 rows
-// in bf16 (past that the tiled MFMA kernel is faster on MI355X), up to 16 in
-// fp32; kRowsPerWave rows per wave.
+// in bf16 (past that the tiled MFMA kernel is faster on MI355X); in fp32 up to 8,
+// and up to 16 when batch x heads alone fills the chip (256 or more).  Below that
+// the tiled kernel's split mode is faster for 9-16 rows (N=1 L=12 S=4096 H=32
+// E=128: 115 -> 79 us; L=16 S=8192: 182 -> 141 us), above it it is not (N=8 L=9
+// S=2048 H=32 E=64: 130 against 148 us).  kRowsPerWave rows per wave.
 constexpr int64_t kRowsMaxL = 16;
+constexpr int64_t kRowsMaxLFew = 8;
 constexpr int kRowsPerWave = 4;
-__host__ __device__ inline bool rows_route(int64_t seq_q, bool bf16) { return seq_q <= (bf16 ? 4 : kRowsMaxL); }
+__host__ __device__ inline bool rows_route(int64_t batch, int64_t seq_q, int64_t heads, bool bf16) {
+  if (bf16) return seq_q <= 4;
+  return seq_q <= kRowsMaxLFew || (seq_q <= kRowsMaxL && batch * heads >= 256);
+}
 constexpr int kRowsWaves = 8;                 // waves per block
 constexpr int64_t kRowsTargetBlocks = 256;    // blocks that keep every CU streaming
 constexpr int64_t kRowsMaxSplits = 64;
@@ -92,7 +99,7 @@ constexpr int64_t kTiledMinKeys = 256;
 constexpr int64_t kTiledMaxSplits = 64;
 __host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads,
                                                 bool bf16, bool causal) {
-  if (rows_route(seq_q, bf16)) return 1;
+  if (rows_route(batch, seq_q, heads, bf16)) return 1;
   if (bf16 && causal && seq_k < 2 * seq_q) return 1;
   const int64_t bm = bf16 ? 256 : 128;
   const int64_t items = batch * heads * ((seq_q + bm - 1) / bm);

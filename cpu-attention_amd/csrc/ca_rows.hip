@@ -1,5 +1,6 @@
 // flash_attn_func for calls with few query rows (rows_route(): up to 4 rows in
-// bf16, 16 in fp32): split-K over key chunks.
+// bf16; in fp32 up to 8, or 16 with 256 or more (batch, head) pairs): split-K
+// over key chunks.
 //
 // With few rows the matrix cores have almost nothing to do; the call is bound by
 // reading K and V once (about one FLOP per byte).  The reference routes such
@@ -596,7 +597,7 @@ static int64_t rows_call_splits(const FlashParams& p, int E, bool bf16) {
 // tiled kernel's split mode.
 int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, int E,
                                    bool bf16) {
-  if (!rows_route(seq_q, bf16)) return tiled_workspace_bytes(batch, seq_q, seq_k, heads, E, bf16, false);
+  if (!rows_route(batch, seq_q, heads, bf16)) return tiled_workspace_bytes(batch, seq_q, seq_k, heads, E, bf16, false);
   int64_t splits = rows_splits(batch, seq_q, seq_k, heads, E, bf16);
   if (rows_heads_shapes(seq_q, seq_k, heads, E, bf16)) {
     const int64_t hs = rows_heads_splits(batch, seq_k, heads, E, bf16);
@@ -607,7 +608,7 @@ int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, 
 }
 
 void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int E, bool bf16) {
-  const int64_t splits = rows_route(p.seq_q, bf16) ? rows_call_splits(p, E, bf16)
+  const int64_t splits = rows_route(p.batch, p.seq_q, p.heads, bf16) ? rows_call_splits(p, E, bf16)
                                                    : tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, bf16, p.causal != 0);
   p.part_acc = static_cast<float*>(ws);
   p.part_ml = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.batch * p.heads * p.seq_q * splits * E * 4)

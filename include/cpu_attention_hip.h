@@ -159,7 +159,8 @@ int ca_decode_noalloc(const ca_decode_args* args, void* stream);
  * bottom-right aligned: query i sees keys j <= i + seq_k - seq_q; a row that sees
  * no key is exactly 0.  out is a contiguous [batch, seq_q, H, E] in the input
  * dtype.  Calls whose keys are split over several blocks leave partials in the
- * workspace: few-row calls (seq_q <= 4 bf16, <= 16 fp32), and calls with fewer
+ * workspace: few-row calls (seq_q <= 4 bf16; <= 8 fp32, or <= 16 with batch x
+ * heads >= 256), and calls with fewer
  * than 256 query blocks of 256 rows (bf16) or 512 of 128 rows (fp32) over long
  * key ranges (bf16 causal calls only with at least twice as many keys as rows).
  * Pass at least the bytes ca_flash_workspace_bytes() asks for (0 means none is

@@ -124,7 +124,8 @@ def test_entries_decline_malformed_calls_without_a_gpu():
 @pytest.mark.parametrize("dtype,d,chunk", [(1, 32, 64), (1, 64, 32), (1, 128, 16),
                                            (0, 32, 32), (0, 64, 16), (0, 128, 8)])
 def test_flash_workspace_for_few_rows(dtype, d, chunk):
-    """Few query rows (up to 4 in bf16, 16 in fp32) go to blocks of 8 waves per
+    """Few query rows (up to 4 in bf16; in fp32 up to 8, or 16 when batch x heads
+    is 256 or more) go to blocks of 8 waves per
     (batch, head, row group: 1 row for single-row calls, else 4); chunks of 4 load
     steps (16-byte slices, 64 lanes).  Only when those blocks number fewer than 256
     are a row group's chunks split over more blocks (at most one chunk per wave and
@@ -133,7 +134,7 @@ def test_flash_workspace_for_few_rows(dtype, d, chunk):
     lib = K.load_library()
 
     def expect(b, sq, sk, h):
-        if sq > (4 if dtype == 1 else 16):
+        if sq > (4 if dtype == 1 else 16 if b * h >= 256 else 8):
             return tiled(b, sq, sk, h, d, dtype)
         blocks = b * h * -(-sq // (1 if sq == 1 else 4))
         splits = 1 if blocks >= 256 else -(-256 // blocks)

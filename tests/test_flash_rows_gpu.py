@@ -1,4 +1,5 @@
-"""flash_attn_func calls with few query rows (up to 4 in bf16, 16 in fp32), which
+"""flash_attn_func calls with few query rows (up to 4 in bf16; in fp32 up to 8, or
+16 when batch x heads is 256 or more), which
 take the split-K few-rows route, against the float64 oracle.  Covers every head
 dim and dtype, key lengths at and past the chunk edges (one chunk, several, a
 partial last one), single rows and row groups of 4 with a partial last group,
@@ -30,19 +31,23 @@ def run(b, sq, sk, h, d, dtype, causal, seed, device, scale=None):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("d", [32, 64, 128])
-@pytest.mark.parametrize("sq", [1, 2, 3, 4, 5, 16])
+@pytest.mark.parametrize("sq", [1, 2, 3, 4, 5, 8, 16])
 @pytest.mark.parametrize("sk", [1, 31, 32, 33, 128, 129, 300, 1100])
 @pytest.mark.parametrize("causal", [True, False])
 def test_few_rows_shapes(cuda, dtype, d, sq, sk, causal):
     run(2, sq, sk, 3, d, dtype, causal, seed=sq * 10000 + sk * 10 + d, device=cuda)
 
 
-@pytest.mark.parametrize("dtype,sq", [(torch.bfloat16, 4), (torch.bfloat16, 5),
-                                      (torch.float32, 16), (torch.float32, 17)])
-def test_route_boundary(cuda, dtype, sq):
+@pytest.mark.parametrize("dtype,sq,h", [(torch.bfloat16, 4, 4), (torch.bfloat16, 5, 4),
+                                        (torch.float32, 8, 4), (torch.float32, 9, 4),
+                                        (torch.float32, 13, 128), (torch.float32, 16, 128),
+                                        (torch.float32, 17, 128)])
+def test_route_boundary(cuda, dtype, sq, h):
     """The last row count of the few-rows route and the first of the tiled one
-    both agree with the oracle."""
-    run(2, sq, 700, 4, 64, dtype, True, seed=sq, device=cuda)
+    both agree with the oracle: bf16 4 | 5; fp32 8 | 9 with 8 (batch, head) pairs,
+    and 16 | 17 with 256 pairs (13 and 16 rows: row groups of 4, the last one
+    partial or full)."""
+    run(2, sq, 700, h, 64, dtype, True, seed=sq, device=cuda)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
