@@ -13,9 +13,10 @@
 // V^T with ds_read_b64_tr_b16 from the row-major V tile.
 //   S^T = K Q^T   32x32x16 MFMAs with keys as rows and queries as columns, so a
 //                 lane ends up owning one query and 16 keys of each 32-key half;
-//   softmax       per lane (its query) against a max fixed at the first tile;
-//                 rows whose later logits outgrow it by more than 64 in log2
-//                 units are redone by a safe pass with a running max;
+//   softmax       per lane (its query) against a max fixed 64 log2 units above
+//                 the first tile's; rows whose later logits outgrow the first
+//                 tile's by more than about 123 are redone by a safe pass with a
+//                 running max;
 //   O^T += V^T P^T the probabilities are already in the B-operand layout of the
 //                 MFMA (no LDS round trip); P is rounded to bf16 as the reference's
 //                 bf16 policy does (flash_vec.mojo:255-259), fp32 accumulation.
@@ -573,8 +574,16 @@ struct P64Rows {
     }
   }
 
-  // Fixes each row's max at tile 0's (every row that sees any key sees key 0),
-  // in scaled log2 units as the reference takes it.
+  // Fixes each row's max at kMaxLift above tile 0's (every row that sees any key
+  // sees key 0), in scaled log2 units as the reference takes it.  The softmax is
+  // the same for any max; the lift only moves the window of logits the fixed max
+  // serves exactly.  p of tile 0's largest logit is 2^-64, so p stays a normal
+  // fp32 (and bf16) for logits down to 62 below it: smaller ones weigh less than
+  // 2^-62 against that key and may flush to 0.  Upwards, a lane's sum of p over a
+  // tile stays within the walk's 2^64 headroom for logits up to about 123 above
+  // tile 0's max (64 without the lift); only rows whose logits outgrow that go
+  // through the safe pass.
+  static constexpr float kMaxLift = 64.f;
   __device__ __forceinline__ void fix_max(float c) {
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
@@ -583,7 +592,7 @@ struct P64Rows {
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[0][cb][kt][r]);
-      m[cb] = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+      m[cb] = fmaxf(mx, __shfl_xor(mx, 32)) * c + kMaxLift;
       nmu[cb] = m[cb] == -INFINITY ? 0.f : -m[cb];
     }
   }
@@ -984,10 +993,11 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
       };
       int t = 0;
       if (nkt_w > 0) {
-        // Tile 0: its S, the row max fixed at its own (never refreshed: the sum
-        // of a lane's p over a tile stays below 2^64 unless a later logit
-        // exceeds the fixed max by about 64 in log2 units, which `bad` records
-        // for the safe pass), then the softmax of tile 0 beside the S of tile 1.
+        // Tile 0: its S, the row max fixed 64 above its own (never refreshed:
+        // the sum of a lane's p over a tile stays below 2^64 unless a later
+        // logit exceeds tile 0's max by about 123 in log2 units, which `bad`
+        // records for the safe pass), then the softmax of tile 0 beside the S of
+        // tile 1.
         w.template step<1, false, true, false>(Vs, kbuf(0), a.c, [] {});
         P64Rows<E>::mfma_guard();
         w.template apply_mask<0>(a, kbeg, 0);
