@@ -87,9 +87,13 @@ extern "C" int64_t ca_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads
                          decode_tile_keys(rows, page_table_width, page_size, head_dim));
 }
 
-// ca_decode and ca_decode_noalloc.  noalloc: the split-K scratch is the library's
-// fixed buffer; a call whose partials with the usual tile size do not fit takes
-// 256-key tiles (fewer partials per row) if those fit.
+// ca_decode and ca_decode_noalloc.  The split-K scratch is the caller's workspace,
+// or for noalloc the library's fixed buffer.  A call whose partials with the
+// preferred tile size do not fit the scratch it has takes 256-key tiles (fewer
+// partials per row) if those fit.  With one tile size the need grows with the
+// rows, so a workspace sized by ca_decode_workspace_bytes for the largest batch
+// holds every smaller batch of the same page table, whichever tile size the
+// smaller batch would prefer.
 static int decode_entry(const ca_decode_args* a, void* stream, bool noalloc) {
   if (!a || !dtype_ok(a->dtype) || !head_dim_ok(a->head_dim) || !page_ok(a->page_size))
     return CA_DECLINED;
@@ -99,11 +103,17 @@ static int decode_entry(const ca_decode_args* a, void* stream, bool noalloc) {
   // The tile size and the split-K scratch it needs depend on the shapes only; the
   // no-allocation entry refuses a call its buffer cannot hold before anything else.
   const int64_t rows = a->num_seqs * a->num_heads;
+  const int64_t have = noalloc ? CA_DECODE_NOALLOC_SCRATCH_BYTES
+                               : (a->workspace && aligned16(a->workspace) && a->workspace_bytes > 0
+                                      ? a->workspace_bytes : 0);
   int tile_keys = decode_tile_keys(rows, a->page_table_width, a->page_size, a->head_dim);
   int64_t need = decode_ws_bytes(rows, a->head_dim, a->page_size, a->page_table_width, tile_keys);
-  if (noalloc && need > CA_DECODE_NOALLOC_SCRATCH_BYTES && tile_keys != kDecodeLongTile) {
-    tile_keys = kDecodeLongTile;
-    need = decode_ws_bytes(rows, a->head_dim, a->page_size, a->page_table_width, tile_keys);
+  if (need > have && tile_keys != kDecodeLongTile) {
+    const int64_t need_long = decode_ws_bytes(rows, a->head_dim, a->page_size, a->page_table_width, kDecodeLongTile);
+    if (need_long <= have || noalloc) {
+      tile_keys = kDecodeLongTile;
+      need = need_long;
+    }
   }
   if (noalloc && need > CA_DECODE_NOALLOC_SCRATCH_BYTES) return CA_SCRATCH_EXCEEDED;
   if (!a->q || !a->k_cache || !a->v_cache || !a->lens || !a->page_table || !a->out)
@@ -236,6 +246,9 @@ extern "C" int ca_flash(const ca_flash_args* a, void* stream) {
   p.c = a->scale * kLog2e;
   p.causal = a->causal ? 1 : 0;
   if (a->workspace_bytes < 0) return CA_DECLINED;
+  // The split kernels write their partials with 16-byte stores.
+  if (a->workspace && !aligned16(a->workspace) && flash_call_splits(p, (int)a->head_dim, a->dtype == CA_BF16) > 1)
+    return CA_DECLINED;
   flash_rows_workspace(p, a->workspace, a->workspace_bytes, (int)a->head_dim, a->dtype == CA_BF16);
   return flash_launch(p, (int)a->head_dim, a->dtype == CA_BF16, static_cast<hipStream_t>(stream));
 }

@@ -38,48 +38,10 @@
 // to the next, but made a call after a cache flush 11% slower: 4096 rows,
 // 287 against 258 us.  A model's other layers pass through the caches between two
 // steps of one layer, so the flushed case is the one kept.)
-#include <atomic>
-#include <mutex>
-
 #include "ca_device.h"
 #include "ca_internal.h"
 
-// The split-K scratch of ca_decode_noalloc: a fixed array in device memory, one
-// copy per GPU (each GPU that runs this library holds it until the process
-// ends).  Host code never names it as a kernel argument or copy target (on the
-// host the name is only a stand-in for the symbol): decode_noalloc_scratch()
-// resolves its device address per GPU, and that address is what the kernels get.
-static __device__ __align__(256) unsigned char scratch[CA_DECODE_NOALLOC_SCRATCH_BYTES];
-
 namespace ca {
-
-namespace {
-constexpr int kMaxDevices = 64;
-std::atomic<void*> g_scratch[kMaxDevices];
-std::mutex g_scratch_mu;
-}  // namespace
-
-// The current device's copy of `scratch`, looked up once per device (with that
-// device current) and remembered.
-int decode_noalloc_scratch(void** ptr) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return CA_HIP_ERROR - (int)e;
-  if (dev < 0 || dev >= kMaxDevices) return CA_DECLINED;
-  void* p = g_scratch[dev].load(std::memory_order_acquire);
-  if (!p) {
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    p = g_scratch[dev].load(std::memory_order_relaxed);
-    if (!p) {
-      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-      if (e != hipSuccess) return CA_HIP_ERROR - (int)e;
-      if (!p) return CA_HIP_ERROR;
-      g_scratch[dev].store(p, std::memory_order_release);
-    }
-  }
-  *ptr = p;
-  return CA_OK;
-}
 
 constexpr int kTile = kDecodeLongTile;  // keys per long tile
 constexpr int kShortTile = 64;           // keys per short tile

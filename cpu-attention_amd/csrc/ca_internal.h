@@ -138,6 +138,9 @@ int decode_noalloc_scratch(void** ptr);
 int flash_launch(const FlashParams& p, int head_dim, int bf16, hipStream_t stream);
 int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, int head_dim,
                                    bool bf16);
+// Splits of the keys the call's kernels use (1: no workspace); p's shapes and
+// causal flag must be set.
+int64_t flash_call_splits(const FlashParams& p, int head_dim, bool bf16);
 void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int head_dim, bool bf16);
 int flash_rows_launch(const FlashParams& p, int head_dim, int bf16, hipStream_t stream);
 // Merges each row's `splits` partials (p.part_acc / p.part_ml) into p.out.

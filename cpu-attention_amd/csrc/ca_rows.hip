@@ -607,9 +607,13 @@ int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, 
   return batch * heads * seq_q * splits * (E + 2) * 4;
 }
 
+int64_t flash_call_splits(const FlashParams& p, int E, bool bf16) {
+  return rows_route(p.batch, p.seq_q, p.heads, bf16) ? rows_call_splits(p, E, bf16)
+                                                     : tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, bf16, p.causal != 0);
+}
+
 void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int E, bool bf16) {
-  const int64_t splits = rows_route(p.batch, p.seq_q, p.heads, bf16) ? rows_call_splits(p, E, bf16)
-                                                   : tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, bf16, p.causal != 0);
+  const int64_t splits = flash_call_splits(p, E, bf16);
   p.part_acc = static_cast<float*>(ws);
   p.part_ml = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.batch * p.heads * p.seq_q * splits * E * 4)
                  : nullptr;

@@ -128,6 +128,15 @@ typedef struct ca_decode_args {
   int64_t new_tokens;  /* tokens per sequence in k_new/v_new (0 or 1: one) */
 } ca_decode_args;
 
+/* ca_decode_workspace_bytes: the split-K scratch a call of these shapes needs
+ * with its preferred tile size (0: none; rows whose page table holds at most one
+ * block of tiles, 512 keys with 64-key tiles or 2048 with 256-key tiles, need
+ * none).  It is not monotonic in num_seqs: the preferred tile size depends on the
+ * number of rows.  ca_decode therefore takes 256-key tiles when the workspace it
+ * is given is too small for the preferred ones but holds those; with one tile
+ * size the need grows with the rows, so a workspace sized once for the largest
+ * batch of a page table serves every smaller batch (its output may then differ
+ * from the preferred tiles' in the last bits, within the same tolerance). */
 int64_t ca_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t head_dim,
                                   int64_t page_size, int64_t page_table_width);
 int ca_decode(const ca_decode_args* args, void* stream);
@@ -137,15 +146,18 @@ int ca_decode(const ca_decode_args* args, void* stream);
  * memory at call time (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments and results as ca_decode;
  * args->workspace and args->workspace_bytes are ignored.  The split-K scratch
- * is a fixed device array inside the library, CA_DECODE_NOALLOC_SCRATCH_BYTES
- * (32 MiB) per GPU, held from the first call on that GPU until the process
- * ends; its address is resolved once per device (the current device at the
- * call; `stream` must belong to it).  A call whose ca_decode_workspace_bytes(...)
- * exceeds that size runs with 256-key tiles (fewer partials per row; its output
- * may then differ from ca_decode's in the last bits, within the same tolerance);
- * if those still do not fit, it returns CA_SCRATCH_EXCEEDED and enqueues nothing
- * (32 MiB covers, e.g., 4096 rows of E=128 up to 30,720 keys of page-table
- * capacity; rows of up to 2048 keys need none).  Every call
+ * is a fixed device array, CA_DECODE_NOALLOC_SCRATCH_BYTES (32 MiB) per GPU, in
+ * a code object of its own that HIP loads on a device at the first
+ * ca_decode_noalloc call there that needs scratch (processes that never call it
+ * do not reserve it); it is then held until the process ends.  Its address is
+ * resolved once per device (the current device at the call; `stream` must
+ * belong to it).  A call whose ca_decode_workspace_bytes(...) exceeds that size
+ * runs with 256-key tiles (fewer partials per row; its output may then differ
+ * from ca_decode's in the last bits, within the same tolerance); if those still
+ * do not fit, it returns CA_SCRATCH_EXCEEDED and enqueues nothing (32 MiB
+ * covers, e.g., 4096 rows of E=128 up to 30,720 keys of page-table capacity).
+ * Rows whose page table holds at most one block of tiles (512 keys with 64-key
+ * tiles, 2048 with 256-key tiles) need no scratch.  Every call
  * on a GPU shares that GPU's one buffer: calls that overlap on one GPU (two
  * streams, or two host threads) race on it and must be serialised by the
  * caller.  The buffer needs no clearing: each call writes every partial it
@@ -165,7 +177,9 @@ int ca_decode_noalloc(const ca_decode_args* args, void* stream);
  * key ranges (bf16 causal calls only with at least twice as many keys as rows).
  * Pass at least the bytes ca_flash_workspace_bytes() asks for (0 means none is
  * needed; it answers for non-causal calls, which split at least as much; a
- * shorter workspace declines the call).  The
+ * shorter workspace declines the call), 16-byte aligned (256 recommended; a
+ * misaligned one declines a call that uses it); its contents need not be
+ * initialised.  The
  * reference's entry grows its workspace on request the same way
  * (flash_attn_interface.py:186-193). */
 typedef struct ca_flash_args {

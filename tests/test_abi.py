@@ -118,6 +118,12 @@ def test_entries_decline_malformed_calls_without_a_gpu():
     assert lib.ca_decode_workspace_bytes(4, 32, 64, 32, 64) == partials(128, 4, 64)  # < 256 rows
     assert lib.ca_decode_workspace_bytes(8, 32, 64, 32, 65) == partials(256, 5, 64)  # > 2048 keys
     assert lib.ca_decode_workspace_bytes(1, 32, 128, 16, 32) == 0          # 512 keys: one block
+    # not monotonic in the batch: 8 sequences of H=32 over 2048 keys prefer 256-key
+    # tiles (no partials), 7 prefer 64-key tiles (ca_decode then takes 256-key tiles
+    # when its workspace holds only theirs), 11 exceed 80 Mi K elements
+    assert lib.ca_decode_workspace_bytes(8, 32, 128, 16, 128) == 0
+    assert lib.ca_decode_workspace_bytes(7, 32, 128, 16, 128) == partials(224, 4, 128)
+    assert lib.ca_decode_workspace_bytes(11, 32, 128, 16, 128) == partials(352, 4, 128)
     assert lib.ca_flash_workspace_bytes(1, 1, 1, 1, 64, 1) == 0
 
 

@@ -119,28 +119,31 @@ def test_cfg4_cross_shape(cuda):
 def test_cfg4_prefill_full_size_sampled(cuda):
     """BASELINE cfg4: N=4 L=S=4096 H=32 E=128 causal bf16, q/k/v strided chunks of a
     fused [N*L, 3*H*E] projection.  The whole output is computed; the float64 oracle
-    checks sampled (batch, head) pairs on sampled rows (first, last, tile edges,
-    random)."""
+    checks every one of the 128 (batch, head) pairs, on one row of each 256-row
+    query block (a different offset per pair and block, so both passes of every
+    causal pair, every wave's rows and every block of the XCD schedule are seen)
+    and on the first and last rows, plus tile and block edges of a few pairs."""
     N, L, H, E = 4, 4096, 32, 128
     g = torch.Generator(device=cuda).manual_seed(4)
     qkv = torch.randn(N * L, 3 * H * E, generator=g, device=cuda).to(torch.bfloat16)
     q, k, v = (qkv[:, i * H * E:(i + 1) * H * E].view(N, L, H, E) for i in range(3))
     out = flash_attn_func(q, k, v, causal=True)
     assert torch.isfinite(out).all()
-    # Rows at the edges of the 64-key tiles and 256-row query blocks (both passes
-    # of a causal pair), and random ones; each row's reference is the oracle over
-    # exactly the keys it sees (j <= i at L == S), under the reference's gate and
-    # the north star's.
-    rng = np.random.default_rng(4)
-    rows = sorted({0, 1, 63, 64, 255, 256, 2047, 2048, 3839, 3840, 4094, 4095,
-                   *rng.integers(0, L, 12).tolist()})
-    pairs = [(0, 0), (1, 17), (3, 31), (2, 5), (0, 30), (3, 8)]
-    for b, h in pairs:
-        kb, vb = values(k[b:b + 1, :, h:h + 1]), values(v[b:b + 1, :, h:h + 1])
-        got = np.stack([values(out[b, i, h]) for i in rows])
-        ref = np.stack([attention(values(q[b:b + 1, i:i + 1, h:h + 1]), kb[:, :i + 1], vb[:, :i + 1],
-                                  E ** -0.5)[0, 0, 0] for i in rows])
-        assert_close(torch.from_numpy(got), ref, torch.bfloat16, paged=False)
+    # Each row's reference is the oracle over exactly the keys it sees (j <= i at
+    # L == S), under the reference's gate and the north star's.
+    edges = [1, 63, 64, 255, 256, 2047, 2048, 3839, 3840, 4094]
+    for b in range(N):
+        for h in range(H):
+            rows = [0, L - 1] + [256 * j + (37 * j + 11 * b + 5 * h + 3) % 256 for j in range(L // 256)]
+            if (b * H + h) % 29 == 0:
+                rows += edges
+            rows = sorted(set(rows))
+            kb, vb = values(k[b:b + 1, :, h:h + 1]), values(v[b:b + 1, :, h:h + 1])
+            qb = values(q[b:b + 1, :, h:h + 1])
+            got = values(out[b, rows, h])
+            ref = np.stack([attention(qb[:, i:i + 1], kb[:, :i + 1], vb[:, :i + 1], E ** -0.5)[0, 0, 0]
+                            for i in rows])
+            assert_close(torch.from_numpy(got), ref, torch.bfloat16, paged=False)
 
 
 @pytest.mark.parametrize("d", [32, 64, 128])

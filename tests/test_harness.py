@@ -76,3 +76,32 @@ def test_one_row_end_to_end(cuda, tmp_path):
     # the comparator (torch SDPA's fused kernels) agrees with ours
     if row.get("ref"):
         assert row["max_diff"] < 5e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(900)
+def test_one_row_with_counters(cuda, tmp_path):
+    """The same row with --counters: its rocprofv3 passes (kernel trace, FETCH_SIZE,
+    WRITE_SIZE, MfmaUtil) run in child processes, and every column they add is
+    there and consistent with the row: device time within the event-timed call,
+    HBM bytes between half and ten times the row's algorithmic bytes (q, k, v
+    read and out written once), the sum of fetch and write, and an MFMA-busy
+    percentage in (0, 100]."""
+    import shutil
+    if shutil.which("rocprofv3") is None:
+        pytest.skip("rocprofv3 is not on PATH")
+    out = tmp_path / "row.json"
+    print("harness row with --counters", flush=True)
+    r = subprocess.run([sys.executable, os.path.join(BENCH, "bench.py"), "--json", str(out), "--table", "reference",
+                        "--only", "N=1 L=128 S=128 H=16 E=64", "--dtype", "bf16", "--counters"],
+                       capture_output=True, text=True, timeout=800, cwd=ROOT, env=dict(os.environ, TMPDIR="/tmp"))
+    assert r.returncode == 0, r.stderr[-2000:]
+    (row,) = json.loads(out.read_text())["rows"]
+    c = row["counters"]
+    assert set(c) >= {"kernel_us", "fetch_bytes", "write_bytes", "hbm_bytes", "mfma_util_pct"}, (c, r.stdout[-2000:])
+    assert 0 < c["kernel_us"] <= row["timing"]["ours"]["gpu"]["max"]
+    io = 1 * 128 * 16 * 64 * 2  # one of q, k, v, out in bf16
+    assert 0.5 * 3 * io <= c["fetch_bytes"] <= 10 * 3 * io
+    assert 0.5 * io <= c["write_bytes"] <= 10 * io
+    assert c["hbm_bytes"] == pytest.approx(c["fetch_bytes"] + c["write_bytes"])
+    assert 0 < c["mfma_util_pct"] <= 100
