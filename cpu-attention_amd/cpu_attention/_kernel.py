@@ -577,9 +577,12 @@ def workspace(nbytes=0):
 
     Keyed by stream because calls on two streams would otherwise write the same
     partials at once.  A buffer that is outgrown is kept (not returned to the
-    allocator) until the process ends, since a captured graph may still name its
-    address.  The package's own ``flash_attn_func`` does not use this: it
-    allocates the scratch per call on the current stream."""
+    allocator), since a captured graph may still name its address: the buffers
+    of a (thread, device, stream) stay until ``release_workspace()`` drops them or
+    the process ends, so a process that keeps creating threads or streams should
+    release each one's buffers once nothing (no graph) uses them.  The package's
+    own ``flash_attn_func`` does not use this: it allocates the scratch per call
+    on the current stream."""
     if not torch.cuda.is_available():
         return 0, 0
     dev = torch.cuda.current_device()
@@ -592,3 +595,18 @@ def workspace(nbytes=0):
         if not held:
             return 0, 0
         return held[-1].data_ptr(), held[-1].numel()
+
+
+def release_workspace(all_streams=False):
+    """Drops the calling thread's ``workspace()`` buffers on the current device:
+    those of the current stream, or of every stream with ``all_streams``.  The
+    caller vouches that no pending call or captured graph still uses them (their
+    memory goes back to torch's allocator).  Returns how many were dropped."""
+    if not torch.cuda.is_available():
+        return 0
+    dev = torch.cuda.current_device()
+    me = threading.get_ident()
+    stream = _stream(torch.device("cuda", dev))
+    with _WS_LOCK:
+        keys = [k for k in _WS if k[0] == me and k[1] == dev and (all_streams or k[2] == stream)]
+        return sum(len(_WS.pop(k)) for k in keys)

@@ -152,6 +152,14 @@ def test_engine_workspace_per_stream(cuda):
         b = K.workspace(10)
         assert b[0] != a[0]
     assert K.workspace(10) == a
+    # releasing the side stream's buffers leaves the current stream's alone
+    with torch.cuda.stream(st):
+        assert K.release_workspace() == 1
+        assert K.workspace() == (0, 0)
+    assert K.workspace() == a
+    K.workspace(4 * a[1])  # outgrown: both buffers stay until released
+    assert K.release_workspace(all_streams=True) == 2
+    assert K.workspace() == (0, 0)
 
 
 def test_native_entry_reports_the_workspace_it_needs(cuda):
