@@ -1046,11 +1046,17 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
                          slot0, splits);
       if (any_bad) {
         const SplitOut so{p.part_acc, p.part_ml, slot0, splits, kbeg};
-        bf16_safe_pass_p64<E>(a, bad, so);
+        const Bf16Pass pa = a;
+        bf16_safe_pass_p64<E>(pa, bad, so);
       }
     } else {
       if (!bad) w.store_staged(a, reinterpret_cast<char*>(smem) + wv * P64Rows<E>::kStageBytes);
-      if (any_bad) bf16_safe_pass_p64<E>(a, bad);
+      if (any_bad) {
+        // The call takes its arguments through the stack: a copy made only here
+        // keeps `a` itself in registers, so the fast path writes no scratch.
+        const Bf16Pass pa = a;
+        bf16_safe_pass_p64<E>(pa, bad);
+      }
     }
   }
 }
