@@ -60,7 +60,7 @@ __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b
 // Hardware dispatches workgroup i to XCD i % 8.  Remap so each XCD walks a
 // contiguous range of the logical work ids: neighbouring work (one head's K/V,
 // or neighbouring heads that share cache lines) then meets in one XCD's L2.
-__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nb) {
+__host__ __device__ inline int64_t xcd_remap(int64_t bid, int64_t nb) {
   const int64_t x = bid & 7, slot = bid >> 3;
   const int64_t per = nb >> 3, rem = nb & 7;
   return x * per + (x < rem ? x : rem) + slot;

@@ -38,19 +38,24 @@ constexpr int kBM = 128;  // fp32: query rows per block (4 waves x 32)
 // A tile that starts past the last key (the prefetch after the last tile) has a
 // negative byte count: it becomes an empty window, where every load reads zero
 // without touching memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int64_t bytes) {
-  const int64_t n = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+__host__ __device__ inline int window_bytes(int64_t bytes) {
+  return (int)(bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes));
 }
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, window_bytes(bytes), 0x00020000);
+}
+
+__host__ __device__ inline int imin(int a, int b) { return a < b ? a : b; }
+__host__ __device__ inline int imax(int a, int b) { return a > b ? a : b; }
 
 struct BlockWork {
   int64_t b, h, q0;
 };
 
-__device__ __forceinline__ BlockWork block_work(const FlashParams& p) {
+__host__ __device__ inline BlockWork block_work(const FlashParams& p, int64_t bid) {
   const int64_t nqb = cdiv(p.seq_q, kBM);
   const int64_t nb = p.batch * p.heads * nqb;
-  const int64_t lg = xcd_remap(blockIdx.x, nb);
+  const int64_t lg = xcd_remap(bid, nb);
   const int64_t bh = lg / nqb;
   const int64_t qb = nqb - 1 - (lg - bh * nqb);  // the most expensive causal blocks first
   BlockWork w;
@@ -123,11 +128,11 @@ __host__ __device__ inline bool pair_blocks(const FlashParams& p, int64_t nqb, b
   return items >= 4 * kPairMinBlocks || (items >= 2 * kPairMinBlocks && p.seq_k < 2 * p.seq_q);
 }
 
-__device__ __forceinline__ PairWork pair_work(const FlashParams& p, int bm, bool bf16) {
+__host__ __device__ inline PairWork pair_work(const FlashParams& p, int bm, bool bf16, int64_t bid) {
   const int64_t nqb = cdiv(p.seq_q, bm);
   const bool pair = pair_blocks(p, nqb, bf16);
   const int64_t per = pair ? (nqb + 1) / 2 : nqb;
-  const int64_t lg = xcd_remap(blockIdx.x, p.batch * p.heads * per);
+  const int64_t lg = xcd_remap(bid, p.batch * p.heads * per);
   const int64_t bh = lg / per, j = lg - bh * per;
   PairWork w;
   w.b = bh / p.heads;
@@ -136,6 +141,55 @@ __device__ __forceinline__ PairWork pair_work(const FlashParams& p, int bm, bool
   w.qb1 = j;
   w.n = (pair && w.qb0 != j) ? 2 : 1;
   return w;
+}
+
+// The bf16 tiled kernel's work for block (bx, by) of its grid: a causal pair or
+// one query block (pair_work), or in the split mode (gy splits) query block bx %
+// nqb of (batch, head) bx / nqb and split by of its keys.
+__host__ __device__ inline PairWork bf16_block_work(const FlashParams& p, bool split, int64_t bx) {
+  PairWork pw;
+  if (split) {
+    const int64_t nqb = cdiv(p.seq_q, 256);
+    const int64_t bh = bx / nqb;
+    pw.b = bh / p.heads;
+    pw.h = bh - pw.b * p.heads;
+    pw.qb0 = pw.qb1 = bx - bh * nqb;
+    pw.n = 1;
+  } else {
+    pw = pair_work(p, 256, true, bx);
+  }
+  return pw;
+}
+
+// A pass's rows and keys: query block rows [q0, q0 + 256), keys [kbeg, kend) in
+// nkt tiles of 64 (the split mode's share of them: whole tiles, empty past the
+// pass's last key).
+struct Bf16Geom {
+  int q0, kbeg, kend, nkt;
+};
+__host__ __device__ inline Bf16Geom bf16_pass_geom(const FlashParams& p, const PairWork& pw, int pass, bool split,
+                                                   int sp, int splits) {
+  const int S = (int)p.seq_k, diag = (int)(p.seq_k - p.seq_q);
+  Bf16Geom g;
+  g.q0 = (int)(pass == 0 ? pw.qb0 : pw.qb1) * 256;
+  g.kbeg = 0;
+  g.kend = p.causal ? imin(S, g.q0 + 256 + diag) : S;
+  if (split) {
+    const int chunk = (int)cdiv(cdiv(p.seq_k, 64), splits) * 64;
+    g.kbeg = imin(sp * chunk, imax(g.kend, 0));
+    g.kend = imin(g.kbeg + chunk, g.kend);
+  }
+  g.nkt = g.kend > g.kbeg ? (g.kend - g.kbeg + 63) / 64 : 0;
+  return g;
+}
+// Tiles of the pass's keys [kbeg, kend) that rows [r0, r0 + nrows) walk (S
+// keys, diag = S - L); `clamp` cuts their keys at kend (the split mode's range;
+// a whole pass's kend never cuts a row's).
+__host__ __device__ inline int bf16_row_tiles(int S, int diag, int causal, int kbeg, int kend, int r0, int nrows,
+                                              bool clamp) {
+  int kend_w = causal ? imin(S, r0 + nrows + diag) : S;
+  if (clamp) kend_w = imin(kend_w, kend);
+  return kend_w > kbeg ? (kend_w - kbeg + 63) / 64 : 0;
 }
 
 // What one pass (a query block of one (batch, head)) needs, shared by the fast
@@ -156,13 +210,23 @@ struct Bf16Pass {
 // P % RS.  Pad columns and chunks past the tile's rows get an offset past any
 // window, so they read as zeros without touching memory.
 template <int E, int RS, int NL>
-__device__ __forceinline__ void tile_offsets(int wv4, int lane, int stride, int (&off)[NL]) {
+__host__ __device__ inline void tile_offsets(int wv4, int lane, int stride, int (&off)[NL]) {
   constexpr int CPR = E / 8, BN = FlashBf16Cfg<E>::BN, NWG = FlashBf16Cfg<E>::NWG;
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
     const int P = (NWG * i + wv4) * 64 + lane, r = P / RS, col = P % RS;
     off[i] = (r < BN && col < CPR) ? (r * stride + 8 * col) * 2 : (int)0x80000000;
   }
+}
+
+// The byte window of a key tile whose first row is followed by `rows` rows of
+// the pass's key range (row stride stride2 bytes): a full tile gets 2^31 - 1
+// bytes (its 64 rows lie inside the range; the launcher bounds 64 rows of the
+// stride below 2^31 bytes), a partial one is cut after its last row, one past
+// the range is empty.
+template <int E>
+__host__ __device__ inline int tile_window(int rows, int stride2) {
+  return rows >= FlashBf16Cfg<E>::BN ? 0x7fffffff : (rows <= 0 ? 0 : (rows - 1) * stride2 + E * 2);
 }
 
 // One wave's share of the successive K tiles or V tiles of a pass: rows [k0, k0 + BN) of the source per tile, cut at the pass's key
@@ -213,8 +277,7 @@ struct TileStream {
   // The next tile of the key range.  A window of 2^31 - 1 bytes covers any tile
   // (the launcher bounds BN rows of the stride below 2^31 bytes).
   __device__ __forceinline__ void issue(const int (&off)[NL]) {
-    const int bytes = rows >= BN ? 0x7fffffff : (rows <= 0 ? 0 : (rows - 1) * stride2 + E * 2);
-    issue_window(bytes, off);
+    issue_window(tile_window<E>(rows, stride2), off);
     addr += step;
     rows -= BN;
   }
@@ -839,8 +902,7 @@ __device__ __forceinline__ void bf16_safe_pass_body(const Bf16Pass& a, bool acti
     loads_done_barrier();
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      const int kend_w = min(a.causal ? min(a.S, w[cb].r0 + 32 + a.diag) : a.S, a.kend);
-      const int nkt_w = active && kend_w > kbeg ? (kend_w - kbeg + BN - 1) / BN : 0;
+      const int nkt_w = active ? bf16_row_tiles(a.S, a.diag, a.causal, kbeg, a.kend, w[cb].r0, 32, true) : 0;
       if (t < nkt_w) {
         f32x16 st[2];
         w[cb].logits(Ks, st);
@@ -899,20 +961,9 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  PairWork pw;
-  int sp = 0, splits = 1;
-  if constexpr (SPLIT) {
-    const int64_t nqb = cdiv(p.seq_q, BM);
-    const int64_t bh = blockIdx.x / nqb;
-    pw.b = bh / p.heads;
-    pw.h = bh - pw.b * p.heads;
-    pw.qb0 = pw.qb1 = blockIdx.x - bh * nqb;
-    pw.n = 1;
-    sp = blockIdx.y;
-    splits = gridDim.y;
-  } else {
-    pw = pair_work(p, BM, true);
-  }
+  static_assert(BM == 256 && BN == 64, "bf16_block_work and bf16_pass_geom assume 256-row blocks of 64-key tiles");
+  const PairWork pw = bf16_block_work(p, SPLIT, blockIdx.x);
+  const int sp = SPLIT ? (int)blockIdx.y : 0, splits = SPLIT ? (int)gridDim.y : 1;
   // Positions and token strides fit 32 bits (the launcher declines otherwise).
   Bf16Pass a;
   a.L = (int)p.seq_q;
@@ -939,20 +990,12 @@ __global__ __launch_bounds__(256, 1) void flash_bf16_p64_kernel(FlashParams p) {
   auto vbuf = [&](int t) { return Vs + (t % C::NBUFV) * C::TBUF; };
 
   for (int pass = 0; pass < pw.n; ++pass) {
-    const int q0 = (int)(pass == 0 ? pw.qb0 : pw.qb1) * BM;
-    w.r0 = q0 + 64 * wv;
     // The pass's keys [kbeg, kend_b): all it sees, or this block's split of them
     // (whole tiles; a split past the pass's last key is empty).
-    int kbeg = 0, kend_b = p.causal ? min(S, q0 + BM + diag) : S;
-    if constexpr (SPLIT) {
-      const int chunk = (int)cdiv(cdiv(p.seq_k, BN), splits) * BN;
-      kbeg = min(sp * chunk, max(kend_b, 0));
-      kend_b = min(kbeg + chunk, kend_b);
-    }
-    const int nkt = kend_b > kbeg ? (kend_b - kbeg + BN - 1) / BN : 0;
-    int kend_w = p.causal ? min(S, w.r0 + 64 + diag) : S;
-    if constexpr (SPLIT) kend_w = min(kend_w, kend_b);
-    const int nkt_w = kend_w > kbeg ? (kend_w - kbeg + BN - 1) / BN : 0;
+    const Bf16Geom g = bf16_pass_geom(p, pw, pass, SPLIT, sp, splits);
+    const int q0 = g.q0, kbeg = g.kbeg, kend_b = g.kend, nkt = g.nkt;
+    w.r0 = q0 + 64 * wv;
+    const int nkt_w = bf16_row_tiles(S, diag, p.causal, kbeg, kend_b, w.r0, 64, SPLIT);
     a.q0 = q0;
     a.kend = kend_b;
 
@@ -1075,6 +1118,39 @@ struct FlashF32Cfg {
   static constexpr int LDS_BYTES = 2 * (LDS_K + LDS_V) * 4;
 };
 
+// The fp32 kernel's keys for the query block at row q0: [kbeg, kend) in nkt
+// tiles of 32, all the block sees or its split sp of splits (whole tiles).
+struct F32Keys {
+  int64_t kbeg, kend;
+  int nkt;
+};
+__host__ __device__ inline F32Keys f32_keys(const FlashParams& p, int64_t q0, bool split, int sp, int splits) {
+  const int64_t S = p.seq_k, diag = p.seq_k - p.seq_q, BN = 32;
+  F32Keys k;
+  k.kbeg = 0;
+  k.kend = p.causal ? (S < q0 + kBM + diag ? S : q0 + kBM + diag) : S;
+  if (split) {
+    const int64_t chunk = cdiv(cdiv(S, BN), splits) * BN;
+    const int64_t lo = k.kend > 0 ? k.kend : 0;
+    k.kbeg = sp * chunk < lo ? sp * chunk : lo;
+    k.kend = k.kbeg + chunk < k.kend ? k.kbeg + chunk : k.kend;
+  }
+  k.nkt = k.kend > k.kbeg ? (int)cdiv(k.kend - k.kbeg, BN) : 0;
+  return k;
+}
+// Byte offset of thread tid's 16-byte chunk i of a 32-key tile (rows `stride`
+// floats apart), and the window from the tile at key k0 to the tensor's last key.
+template <int E>
+__host__ __device__ inline int f32_tile_offset(int tid, int i, int64_t stride) {
+  const int c = tid + 256 * i;
+  const int r = c / (E / 4), c4 = c % (E / 4);
+  return (int)((r * stride + 4 * c4) * 4);
+}
+template <int E>
+__host__ __device__ inline int64_t f32_tile_bytes(int64_t S, int64_t k0, int64_t stride) {
+  return ((S - 1 - k0) * stride + E) * 4;
+}
+
 // SPLIT: blockIdx.y is one of gridDim.y splits of the key range, each a run of
 // whole tiles; the block writes unnormalised (O, max, sum) partials of its rows
 // for the combine kernel instead of the output.
@@ -1094,29 +1170,23 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int li = lane & 31, hf = lane >> 5;
   PairWork pw{};
-  if constexpr (PAIR) pw = pair_work(p, kBM, false);
+  if constexpr (PAIR) pw = pair_work(p, kBM, false, blockIdx.x);
 #pragma unroll 1
   for (int pass = 0; pass < (PAIR ? pw.n : 1); ++pass) {
   if (PAIR && pass > 0) __syncthreads();  // the first pass's tile buffers are free again
-  const BlockWork bw = PAIR ? BlockWork{pw.b, pw.h, (pass ? pw.qb1 : pw.qb0) * kBM} : block_work(p);
+  const BlockWork bw = PAIR ? BlockWork{pw.b, pw.h, (pass ? pw.qb1 : pw.qb0) * kBM} : block_work(p, blockIdx.x);
   const int64_t L = p.seq_q, S = p.seq_k, diag = S - L;
   const float* qg = reinterpret_cast<const float*>(p.q) + bw.b * p.qs[0] + bw.h * p.qs[2];
   const float* kg = reinterpret_cast<const float*>(p.k) + bw.b * p.ks[0] + bw.h * p.ks[2];
   const float* vg = reinterpret_cast<const float*>(p.v) + bw.b * p.vs[0] + bw.h * p.vs[2];
 
   const int64_t row = bw.q0 + 32 * wv + li;
-  int64_t kbeg = 0, kend_blk = p.causal ? min<int64_t>(S, bw.q0 + kBM + diag) : S;
-  int sp = 0, splits = 1;
-  if constexpr (SPLIT) {
-    sp = blockIdx.y;
-    splits = gridDim.y;
-    const int64_t chunk = cdiv(cdiv(S, BN), splits) * BN;
-    kbeg = min<int64_t>(sp * chunk, max<int64_t>(kend_blk, 0));
-    kend_blk = min<int64_t>(kbeg + chunk, kend_blk);
-  }
+  const int sp = SPLIT ? (int)blockIdx.y : 0, splits = SPLIT ? (int)gridDim.y : 1;
+  const F32Keys kr_ = f32_keys(p, bw.q0, SPLIT, sp, splits);
+  const int64_t kbeg = kr_.kbeg, kend_blk = kr_.kend;
   // The partial slot of (row, split): O at part_acc[slot * E], (max, sum) at part_ml[2 * slot].
   const int64_t slot = ((bw.b * p.heads + bw.h) * L + row) * splits + sp;
-  const int nkt = kend_blk > kbeg ? (int)cdiv(kend_blk - kbeg, BN) : 0;
+  const int nkt = kr_.nkt;
   if (nkt == 0) {  // every row of the block sees no key of this range: exactly 0
     if (SPLIT && row < L) {
       float* pa = p.part_acc + slot * E;
@@ -1153,14 +1223,12 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
   int koff[C::CH], voff[C::CH];
 #pragma unroll
   for (int i = 0; i < C::CH; ++i) {
-    const int c = tid + 256 * i;
-    const int r = c / (E / 4), c4 = c % (E / 4);
-    koff[i] = (int)((r * p.ks[1] + 4 * c4) * 4);
-    voff[i] = (int)((r * p.vs[1] + 4 * c4) * 4);
+    koff[i] = f32_tile_offset<E>(tid, i, p.ks[1]);
+    voff[i] = f32_tile_offset<E>(tid, i, p.vs[1]);
   }
   auto load_tile = [&](int t) {
     const int64_t k0 = kbeg + (int64_t)t * BN;
-    const int64_t kbytes = ((S - 1 - k0) * p.ks[1] + E) * 4, vbytes = ((S - 1 - k0) * p.vs[1] + E) * 4;
+    const int64_t kbytes = f32_tile_bytes<E>(S, k0, p.ks[1]), vbytes = f32_tile_bytes<E>(S, k0, p.vs[1]);
     const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kg + k0 * p.ks[1], kbytes);
     const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vg + k0 * p.vs[1], vbytes);
 #pragma unroll
@@ -1289,30 +1357,48 @@ static int launch_lds(K kernel, int64_t nb, int threads, int lds, const FlashPar
   return ca_launch_status();
 }
 
-int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
-  if (p.batch * p.heads * p.seq_q == 0) return CA_OK;
+FlashPlan flash_plan(const FlashParams& p, int E, bool bf16) {
+  FlashPlan plan{};
+  if (p.batch * p.heads * p.seq_q == 0) {
+    plan.kind = kPlanNone;
+    return plan;
+  }
+  if (E != 32 && E != 64 && E != 128) return plan;
   // The tile loads address a tile's rows with 32-bit byte offsets from its first
   // row: 64 rows of the token stride must fit (larger strides are declined and
   // the caller copies the tensor).
   const int64_t esz = bf16 ? 2 : 4;
   int64_t ts = p.ks[1] > p.vs[1] ? p.ks[1] : p.vs[1];
   if (p.qs[1] > ts) ts = p.qs[1];
-  if (p.qs[1] < 0 || p.ks[1] < 0 || p.vs[1] < 0 || 64 * (ts + E) * esz >= ((int64_t)1 << 31))
-    return CA_DECLINED;
+  if (p.qs[1] < 0 || p.ks[1] < 0 || p.vs[1] < 0 || 64 * (ts + E) * esz >= ((int64_t)1 << 31)) return plan;
   // Row and key positions are 32-bit inside the kernels.
-  if (p.seq_q >= ((int64_t)1 << 30) || p.seq_k >= ((int64_t)1 << 30)) return CA_DECLINED;
-  if (rows_route(p.batch, p.seq_q, p.heads, bf16 != 0)) return flash_rows_launch(p, E, bf16, stream);
+  if (p.seq_q >= ((int64_t)1 << 30) || p.seq_k >= ((int64_t)1 << 30)) return plan;
+  if (rows_route(p.batch, p.seq_q, p.heads, bf16)) return rows_plan(p, E, bf16);
   // Split mode: one block per (batch, head, query block) and split of its keys,
-  // then the combine of each row's partials into the output.
-  const int64_t splits = tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, bf16 != 0, p.causal != 0);
-  if (splits > 1) {
-    const int64_t need = tiled_workspace_bytes(p.batch, p.seq_q, p.seq_k, p.heads, E, bf16 != 0, p.causal != 0);
-    if (p.part_acc == nullptr || p.part_ml == nullptr || p.workspace_bytes < need) return CA_DECLINED;
-  }
+  // then the combine of each row's partials into the output.  Otherwise one
+  // block per (batch, head) and query-block pair (causal) or query block.
+  plan.kind = bf16 ? kPlanBf16 : kPlanF32;
+  plan.splits = tiled_splits(p.batch, p.seq_q, p.seq_k, p.heads, bf16, p.causal != 0);
+  plan.need = tiled_workspace_bytes(p.batch, p.seq_q, p.seq_k, p.heads, E, bf16, p.causal != 0);
+  plan.split = plan.splits > 1;
+  plan.gy = plan.splits;
+  const int64_t nqb = cdiv(p.seq_q, bf16 ? 256 : kBM);
+  plan.pair = !plan.split && pair_blocks(p, nqb, bf16);
+  plan.gx = p.batch * p.heads * (plan.pair ? (nqb + 1) / 2 : nqb);
+  if (plan.gx > 0x7fffffff || plan.gy > 0xffff) plan.kind = kPlanDeclined;
+  return plan;
+}
+
+int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
+  const FlashPlan plan = flash_plan(p, E, bf16 != 0);
+  if (plan.kind == kPlanNone) return CA_OK;
+  if (plan.kind == kPlanDeclined) return CA_DECLINED;
+  if (plan.need > 0 && (p.part_acc == nullptr || p.part_ml == nullptr || p.workspace_bytes < plan.need))
+    return CA_DECLINED;
+  if (plan.kind == kPlanRows || plan.kind == kPlanRowsHeads) return flash_rows_launch(p, plan, E, bf16, stream);
+  const int64_t nb = plan.gx, splits = plan.splits;
   if (bf16) {
-    const int64_t nqb = cdiv(p.seq_q, FlashP64Cfg<128>::BM);
-    if (splits > 1) {
-      const int64_t nb = p.batch * p.heads * nqb;
+    if (plan.split) {
       int st = CA_DECLINED;
       switch (E) {
         case 32: st = launch_lds(flash_bf16_p64_kernel<32, true>, nb, 64 * FlashP64Cfg<32>::NW, FlashP64Cfg<32>::LDS_BYTES, p, stream, splits); break;
@@ -1322,17 +1408,13 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
       if (st != CA_OK) return st;
       return flash_combine_launch(p, E, bf16, splits, stream);
     }
-    // One block per (batch, head) and query-block pair (causal) or query block.
-    const int64_t nb = p.batch * p.heads * (pair_blocks(p, nqb, true) ? (nqb + 1) / 2 : nqb);
     switch (E) {
       case 32: return launch_lds(flash_bf16_p64_kernel<32, false>, nb, 64 * FlashP64Cfg<32>::NW, FlashP64Cfg<32>::LDS_BYTES, p, stream);
       case 64: return launch_lds(flash_bf16_p64_kernel<64, false>, nb, 64 * FlashP64Cfg<64>::NW, FlashP64Cfg<64>::LDS_BYTES, p, stream);
       case 128: return launch_lds(flash_bf16_p64_kernel<128, false>, nb, 64 * FlashP64Cfg<128>::NW, FlashP64Cfg<128>::LDS_BYTES, p, stream);
     }
   } else {
-    const int64_t nqb = cdiv(p.seq_q, kBM);
-    const int64_t nb = p.batch * p.heads * nqb;
-    if (splits > 1) {
+    if (plan.split) {
       int st = CA_DECLINED;
       switch (E) {
         case 32: st = launch_lds(flash_f32_kernel<32, true, false>, nb, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream, splits); break;
@@ -1342,12 +1424,11 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
       if (st != CA_OK) return st;
       return flash_combine_launch(p, E, bf16, splits, stream);
     }
-    if (pair_blocks(p, nqb, false)) {
-      const int64_t nbp = p.batch * p.heads * ((nqb + 1) / 2);
+    if (plan.pair) {
       switch (E) {
-        case 32: return launch_lds(flash_f32_kernel<32, false, true>, nbp, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream);
-        case 64: return launch_lds(flash_f32_kernel<64, false, true>, nbp, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream);
-        case 128: return launch_lds(flash_f32_kernel<128, false, true>, nbp, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream);
+        case 32: return launch_lds(flash_f32_kernel<32, false, true>, nb, 256, FlashF32Cfg<32>::LDS_BYTES, p, stream);
+        case 64: return launch_lds(flash_f32_kernel<64, false, true>, nb, 256, FlashF32Cfg<64>::LDS_BYTES, p, stream);
+        case 128: return launch_lds(flash_f32_kernel<128, false, true>, nb, 256, FlashF32Cfg<128>::LDS_BYTES, p, stream);
       }
       return CA_DECLINED;
     }

@@ -135,6 +135,20 @@ int64_t decode_tiles(int64_t pt_width, int64_t page, int tile_keys);
 int64_t decode_workspace_slots(int64_t rows, int64_t tiles);
 int decode_launch(const DecodeParams& p, int head_dim, int bf16, hipStream_t stream);
 int decode_noalloc_scratch(void** ptr);
+// How flash_launch runs a call: the kernel, its grid (gy = splits of the keys
+// in the split modes), and whether the combine kernel merges `splits` partials
+// per row afterwards.  kind is kPlanDeclined for a call the kernels cannot take.
+enum { kPlanDeclined = 0, kPlanNone, kPlanRows, kPlanRowsHeads, kPlanBf16, kPlanF32 };
+struct FlashPlan {
+  int kind;
+  int rows_r;      // kPlanRows: query rows per wave group (1 or kRowsPerWave)
+  bool split;      // kPlanBf16 / kPlanF32: keys split over gy blocks
+  bool pair;       // kPlanF32: causal query-block pairs
+  int64_t gx, gy;  // grid
+  int64_t splits;  // > 1: the combine kernel merges this many partials per row
+  int64_t need;    // workspace bytes the partials take
+};
+FlashPlan flash_plan(const FlashParams& p, int head_dim, bool bf16);
 int flash_launch(const FlashParams& p, int head_dim, int bf16, hipStream_t stream);
 int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, int head_dim,
                                    bool bf16);
@@ -142,7 +156,9 @@ int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, 
 // causal flag must be set.
 int64_t flash_call_splits(const FlashParams& p, int head_dim, bool bf16);
 void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int head_dim, bool bf16);
-int flash_rows_launch(const FlashParams& p, int head_dim, int bf16, hipStream_t stream);
+int flash_rows_launch(const FlashParams& p, const FlashPlan& plan, int head_dim, int bf16, hipStream_t stream);
+// The few-rows route's part of flash_plan (p.seq_q within rows_route).
+FlashPlan rows_plan(const FlashParams& p, int head_dim, bool bf16);
 // Merges each row's `splits` partials (p.part_acc / p.part_ml) into p.out.
 int flash_combine_launch(const FlashParams& p, int head_dim, int bf16, int64_t splits, hipStream_t stream);
 

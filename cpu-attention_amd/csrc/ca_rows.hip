@@ -52,10 +52,33 @@ __host__ __device__ inline int64_t rows_chunk_keys(int E, bool bf16) {
 __host__ __device__ inline int rows_per_wave(int64_t seq_q) { return seq_q == 1 ? 1 : kRowsPerWave; }
 
 // Keys row i may see: [0, kend).
-__device__ __forceinline__ int64_t rows_kend(const FlashParams& p, int64_t i) {
+__host__ __device__ inline int64_t rows_kend(const FlashParams& p, int64_t i) {
   if (!p.causal) return p.seq_k;
   const int64_t e = i + 1 + p.seq_k - p.seq_q;
   return e < 0 ? 0 : (e < p.seq_k ? e : p.seq_k);
+}
+
+// Block (bx of gx, split of gy) of the per-head kernel with R rows per group:
+// (batch b, head h), rows [i0, i0 + nr), whose widest key range is kend_g keys in
+// nch chunks of ch.  With one split, neighbouring (batch, head) pairs share an
+// XCD (E = 32 bf16 rows are half a 128-byte line; the other half is the next
+// head's).
+struct RowsWork {
+  int64_t b, h, i0, kend_g, nch;
+  int nr;
+};
+__host__ __device__ inline RowsWork rows_work(const FlashParams& p, int R, int ch, int64_t bx, int64_t gx, int64_t gy) {
+  const int64_t ngroups = cdiv(p.seq_q, R);
+  const int64_t lb = gy == 1 ? xcd_remap(bx, gx) : bx;
+  const int64_t bh = lb / ngroups, rg = lb - bh * ngroups;
+  RowsWork w;
+  w.b = bh / p.heads;
+  w.h = bh - w.b * p.heads;
+  w.i0 = rg * R;
+  w.nr = (int)(p.seq_q - w.i0 < R ? p.seq_q - w.i0 : R);
+  w.kend_g = rows_kend(p, w.i0 + w.nr - 1);
+  w.nch = cdiv(w.kend_g, ch);
+  return w;
 }
 
 // Sum over aligned groups of G lanes; every lane of a group ends with the same
@@ -192,16 +215,11 @@ __global__ __launch_bounds__(64 * kRowsWaves) void flash_rows_kernel(FlashParams
   __shared__ float part[W][R][PS];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t ngroups = cdiv(p.seq_q, R);
-  // One split: neighbouring (batch, head) pairs share an XCD (E = 32 bf16 rows
-  // are half a 128-byte line; the other half is the next head's).
-  const int64_t lb = gridDim.y == 1 ? xcd_remap(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
-  const int64_t bh = lb / ngroups, rg = lb - bh * ngroups;
-  const int64_t b = bh / p.heads, h = bh - b * p.heads;
-  const int64_t i0 = rg * R;
-  const int nr = (int)min<int64_t>(R, p.seq_q - i0);
-  const int64_t kend_g = rows_kend(p, i0 + nr - 1);  // the group's widest key range
-  const int64_t nch = cdiv(kend_g, CH);
+  const RowsWork rw = rows_work(p, R, CH, blockIdx.x, gridDim.x, gridDim.y);
+  const int64_t b = rw.b, h = rw.h, bh = b * p.heads + h, i0 = rw.i0;
+  const int nr = rw.nr;
+  const int64_t kend_g = rw.kend_g;  // the group's widest key range
+  const int64_t nch = rw.nch;
   const int64_t splits = gridDim.y, sp = blockIdx.y;
   const int sl = lane % G;  // this lane's slice of a row
   const int kl = lane / G;  // this lane's key within a load instruction
@@ -371,6 +389,20 @@ __host__ __device__ inline bool rows_heads_route(const FlashParams& p, int E, bo
   return rows_heads_shapes(p.seq_q, p.seq_k, p.heads, E, bf16) && p.qs[2] == E && p.ks[2] == E && p.vs[2] == E;
 }
 
+// Block (bx of gx, split of gy) of the packed-heads kernel: batch b, heads
+// [h0, h0 + hp).
+struct HeadsWork {
+  int64_t b, h0;
+};
+__host__ __device__ inline HeadsWork heads_work(const FlashParams& p, int hp, int64_t bx, int64_t gx, int64_t gy) {
+  const int64_t ng = p.heads / hp;
+  const int64_t lb = gy == 1 ? xcd_remap(bx, gx) : bx;
+  HeadsWork w;
+  w.b = lb / ng;
+  w.h0 = (lb - w.b * ng) * hp;
+  return w;
+}
+
 template <int E, bool BF>
 __global__ __launch_bounds__(64 * kRowsWaves) void flash_rows_heads_kernel(FlashParams p) {
   using S = HeadsShape<E, BF>;
@@ -379,9 +411,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void flash_rows_heads_kernel(Flash
   __shared__ float part[W][HP][PS];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t ng = p.heads / HP;
-  const int64_t lb = gridDim.y == 1 ? xcd_remap(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
-  const int64_t b = lb / ng, h0 = (lb - b * ng) * HP;
+  const HeadsWork hw = heads_work(p, HP, blockIdx.x, gridDim.x, gridDim.y);
+  const int64_t b = hw.b, h0 = hw.h0;
   const int64_t splits = gridDim.y, sp = blockIdx.y;
   const int sl = lane % G;   // this lane's slice of a head row
   const int hl = lane / G;   // this lane's head within the group
@@ -621,13 +652,10 @@ void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int E, bool b
 }
 
 template <int E, bool BF>
-static int rows_launch_t(const FlashParams& p, hipStream_t stream) {
-  const int R = rows_per_wave(p.seq_q);
-  const bool heads = rows_heads_route(p, E, BF);
-  const int64_t gx = heads ? p.batch * (p.heads / HeadsShape<E, BF>::HP) : p.batch * p.heads * cdiv(p.seq_q, R);
-  const int64_t splits = rows_call_splits(p, E, BF);
-  if (gx > 0x7fffffff) return CA_DECLINED;
-  if (heads)
+static int rows_launch_t(const FlashParams& p, const FlashPlan& plan, hipStream_t stream) {
+  const int R = plan.rows_r;
+  const int64_t gx = plan.gx, splits = plan.gy;
+  if (plan.kind == kPlanRowsHeads)
     hipLaunchKernelGGL((flash_rows_heads_kernel<E, BF>), dim3((unsigned)gx, (unsigned)splits), dim3(64 * kRowsWaves),
                        0, stream, p);
   else if (R == 1)
@@ -666,21 +694,30 @@ int flash_combine_launch(const FlashParams& p, int E, int bf16, int64_t splits, 
   return ca_launch_status();
 }
 
-int flash_rows_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
-  const int64_t splits = rows_call_splits(p, E, bf16 != 0);
-  const int64_t need = splits > 1 ? p.batch * p.heads * p.seq_q * splits * (E + 2) * 4 : 0;
-  if (need > 0 && (p.part_acc == nullptr || p.workspace_bytes < need)) return CA_DECLINED;
+FlashPlan rows_plan(const FlashParams& p, int E, bool bf16) {
+  FlashPlan plan{};
+  const bool heads = rows_heads_route(p, E, bf16);
+  plan.kind = heads ? kPlanRowsHeads : kPlanRows;
+  plan.rows_r = rows_per_wave(p.seq_q);
+  plan.gx = heads ? p.batch * (p.heads / rows_heads_per_load(E, bf16)) : p.batch * p.heads * cdiv(p.seq_q, plan.rows_r);
+  plan.gy = plan.splits = rows_call_splits(p, E, bf16);
+  plan.need = plan.splits > 1 ? p.batch * p.heads * p.seq_q * plan.splits * (E + 2) * 4 : 0;
+  if (plan.gx > 0x7fffffff || plan.gy > 0xffff) plan.kind = kPlanDeclined;
+  return plan;
+}
+
+int flash_rows_launch(const FlashParams& p, const FlashPlan& plan, int E, int bf16, hipStream_t stream) {
   if (bf16) {
     switch (E) {
-      case 32: return rows_launch_t<32, true>(p, stream);
-      case 64: return rows_launch_t<64, true>(p, stream);
-      case 128: return rows_launch_t<128, true>(p, stream);
+      case 32: return rows_launch_t<32, true>(p, plan, stream);
+      case 64: return rows_launch_t<64, true>(p, plan, stream);
+      case 128: return rows_launch_t<128, true>(p, plan, stream);
     }
   } else {
     switch (E) {
-      case 32: return rows_launch_t<32, false>(p, stream);
-      case 64: return rows_launch_t<64, false>(p, stream);
-      case 128: return rows_launch_t<128, false>(p, stream);
+      case 32: return rows_launch_t<32, false>(p, plan, stream);
+      case 64: return rows_launch_t<64, false>(p, plan, stream);
+      case 128: return rows_launch_t<128, false>(p, plan, stream);
     }
   }
   return CA_DECLINED;
