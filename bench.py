@@ -80,10 +80,10 @@ METRIC = "decode HBM GB/s + µs/call; prefill TFLOP/s (bf16) vs MI355X roofline"
 # and combine dispatches), and what the same counter read for the run's 1 GiB
 # calibration copy.
 TRAFFIC = {
-    "decode": {"fetch_kib": 543080.5 + 1278.0, "write_kib": 2630.125 + 400.0,
-               "copy_fetch_kib": 524315.438, "copy_write_kib": 1048576.0},
-    "prefill": {"fetch_kib": 313687.062, "write_kib": 152576.0,
-                "copy_fetch_kib": 524315.375, "copy_write_kib": 1048576.0},
+    "decode": {"fetch_kib": 543080.5 + 1310.5, "write_kib": 2630.3 + 400.0,
+               "copy_fetch_kib": 524307.9, "copy_write_kib": 1048576.0},
+    "prefill": {"fetch_kib": 312512.1, "write_kib": 132096.0,
+                "copy_fetch_kib": 524307.9, "copy_write_kib": 1048576.0},
 }
 
 # The reference's published CPU figures (medians at its Python API, L2/L3 flushed,
