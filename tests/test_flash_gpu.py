@@ -148,13 +148,15 @@ def test_cfg4_prefill_full_size_sampled(cuda):
 
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("gap", [40, 100])
+@pytest.mark.parametrize("gap", [40, 100, 180])
 def test_logits_outgrowing_the_first_tile(cuda, d, causal, gap):
     """Keys far past the first 64 whose logits exceed every logit of the first key
-    tile by about `gap` log2 units.  The bf16 kernel's fast walk keeps the first
-    tile's row max, so p reaches about 2^gap: up to 2^64 per tile it carries on
-    (the values are exact, only large), past that those rows are recomputed with a
-    running max (some waves of a block take that path, others do not)."""
+    tile by about `gap` log2 units.  The bf16 kernel's fast walk fixes each row's
+    max 64 units above the first tile's, so p reaches about 2^(gap - 64): up to a
+    tile sum of 2^64 (gaps up to ~123) it carries on (the values are exact, only
+    large), past that those rows are recomputed with a running max (some waves of a
+    block take that path, others do not; at d = 32 the gap spreads widely over the
+    rows, and some p overflow to inf before their wave is redone)."""
     g = torch.Generator().manual_seed(11)
     b, sq, sk, h = 2, 300, 700, 2
     q = (torch.randn(b, sq, h, d, generator=g) + 1.0).bfloat16()
@@ -183,9 +185,9 @@ def test_safe_pass_for_one_pass_of_a_causal_pair(cuda, d, bad_pass):
     b, L, h = 1, 512, 130  # 260 query blocks: paired
     q = torch.randn(b, L, h, d, generator=g) * 0.5 + 1.0
     k = torch.randn(b, L, h, d, generator=g) * 0.5
-    # a key whose logits sit about 100 log2 units above the first tile's (past the
-    # fast walk's 2^64 headroom)
-    big = 104 / (1.4427 * d ** 0.5)
+    # a key whose logits sit about 180 log2 units above the first tile's max (past
+    # the ~123 that the fast walk's fixed max and 2^64 headroom serve)
+    big = 184 / (1.4427 * d ** 0.5)
     if bad_pass == 0:
         k[:, 400] = big  # seen only by rows >= 400 (pass 0)
     else:
@@ -203,8 +205,9 @@ def test_safe_pass_for_one_pass_of_a_causal_pair(cuda, d, bad_pass):
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("causal,sq,h", [(True, 1536, 2), (False, 600, 2), (True, 1536, 44), (False, 600, 86)])
 def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq, h):
-    """Key 100 sits about 100 log2 units above every row's first-tile max, so every
-    wave whose rows all see it fails the fast walk's headroom from tile 1 on, and
+    """Key 100 sits about 180 log2 units above every row's first-tile max (the fast
+    walk serves ~123), so every wave whose rows see it fails the walk's headroom
+    from tile 1 on, and
     whole blocks redo their rows in the safe pass.  Causal, 1536 rows: the pair
     (rows 1280-1535, rows 0-255) fails all of its first pass and part of its second
     (whose first wave never sees key 100).  Non-causal, 600 rows over 1536 keys:
@@ -217,7 +220,7 @@ def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq, h):
     sk = 1536
     q = torch.randn(b, sq, h, d, generator=g) * 0.5 + 1.0
     k = torch.randn(b, sk, h, d, generator=g) * 0.5
-    k[:, 100] = 104 / (1.4427 * d ** 0.5)
+    k[:, 100] = 184 / (1.4427 * d ** 0.5)
     q, k = q.bfloat16().to(cuda), k.bfloat16().to(cuda)
     v = torch.randn(b, sk, h, d, generator=g).bfloat16().to(cuda)
     out = flash_attn_func(q, k, v, causal=causal)
@@ -303,14 +306,14 @@ def test_split_keys_rows_without_keys(cuda, dtype):
 
 @pytest.mark.parametrize("d", [64, 128])
 def test_split_keys_safe_pass(cuda, d):
-    """A key about 100 log2 units above its split's first tile: the waves of the
-    split that holds it redo their rows in the safe pass, which writes partials
-    for the combine like the fast walk."""
+    """A key about 180 log2 units above its split's first tile (the fast walk
+    serves ~123): the waves of the split that holds it redo their rows in the safe
+    pass, which writes partials for the combine like the fast walk."""
     g = torch.Generator().manual_seed(33)
     b, sq, sk, h = 1, 64, 4096, 8
     q = torch.randn(b, sq, h, d, generator=g) * 0.5 + 1.0
     k = torch.randn(b, sk, h, d, generator=g) * 0.5
-    k[:, 2100] = 104 / (1.4427 * d ** 0.5)
+    k[:, 2100] = 184 / (1.4427 * d ** 0.5)
     q, k = q.bfloat16().to(cuda), k.bfloat16().to(cuda)
     v = torch.randn(b, sk, h, d, generator=g).bfloat16().to(cuda)
     for causal in (False, True):
