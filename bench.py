@@ -8,9 +8,12 @@ N=64 H=32 E=128 page 32, cache_seqlens U[17,2047], random-permutation page table
 no append): the north-star decode workload, HBM-bound.  ``value`` is the
 whole-job throughput in algorithmic HBM bytes per second over the K timed steps
 (inputs already resident in HBM), timed between two device synchronisations;
-every step is also bracketed by HIP events on the stream the kernels are
-launched on (torch's current stream), which give ``us_per_call`` and the
-roofline.
+HIP events on the stream the kernels are launched on (torch's current stream)
+bracket the timed region, split into TIMED_CHUNKS runs of consecutive steps, and
+give ``us_per_call`` (the region's event time over K) and the roofline;
+``us_per_call_median`` is the median of the runs' means.  No event sits between
+the calls of a run: an event pair around every call adds ~2 us of GPU time of
+its own.
 
 Clock.  The chip needs tens of milliseconds of continuous work to settle at its
 operating clock (the per-call trace from a cold start, ``--clock-trace``, shows
@@ -72,6 +75,7 @@ BF16_PEAK_TFLOPS = 2500.0
 COPY_BYTES = 1 << 30  # the calibration copy of --profile-pass
 FLUSH_BYTES = 1 << 30  # written between cold samples: > 2 x (256 MB MALL + L2)
 RAMP_S = 0.2  # seconds of back-to-back calls before each leg's warm-up
+TIMED_CHUNKS = 10  # event-timed runs the timed calls are split into
 CPU_BUDGET_S = 8.0  # seconds of back-to-back calls per CPU baseline
 METRIC = "decode HBM GB/s + µs/call; prefill TFLOP/s (bf16) vs MI355X roofline"
 
@@ -133,24 +137,38 @@ def ramp(fn, seconds=RAMP_S):
             return n
 
 
-def timed(fn, steps, warmup, ramp_s=RAMP_S):
-    """Clock ramp, `warmup` untimed calls, then `steps` calls between two device
-    synchronisations, each bracketed by events on the current stream.  Returns
-    (wall seconds over the timed calls, per-call event milliseconds, ramp calls)."""
+def timed(fn, steps, warmup, ramp_s=RAMP_S, chunks=TIMED_CHUNKS):
+    """Clock ramp, `warmup` untimed calls, then `steps` back-to-back calls between
+    two device synchronisations.  Events on the current stream split the timed
+    calls into `chunks` runs of consecutive calls (no event between the calls of
+    a run: an event pair around every call adds its own ~2 us of GPU time, which
+    is a tenth of a small call).  Returns (wall seconds over the timed calls, the
+    event milliseconds per call of each run, ramp calls); the mean call is the
+    event time of the whole region over `steps`."""
     nramp = ramp(fn, ramp_s) if ramp_s > 0 else 0
     for _ in range(warmup):
         fn()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
+    n = max(1, min(chunks, steps))
+    sizes = [steps // n + (1 if i < steps % n else 0) for i in range(n)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for a, b in ev:
-        a.record()
-        fn()
-        b.record()
+    ev[0].record()
+    for i, size in enumerate(sizes):
+        for _ in range(size):
+            fn()
+        ev[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return wall, [a.elapsed_time(b) for a, b in ev], nramp
+    return wall, [ev[i].elapsed_time(ev[i + 1]) / size for i, size in enumerate(sizes)], nramp
+
+
+def region_ms(ms, steps):
+    """Mean event milliseconds per call over the whole timed region (runs weighted
+    by their call counts)."""
+    n = len(ms)
+    sizes = [steps // n + (1 if i < steps % n else 0) for i in range(n)]
+    return sum(m * s for m, s in zip(ms, sizes)) / steps
 
 
 class Flush:
@@ -196,7 +214,7 @@ def measure(fn, flush, work, unit, steps=100, warmup=10, cold_samples=15, peak=N
     """One config entry: warm and cold device time, API wall time, and the rate
     of `work` (bytes or FLOP per call) against `peak`."""
     _, ms, nramp = timed(fn, steps, warmup, ramp_s=0.05)
-    warm = float(np.mean(ms))
+    warm = region_ms(ms, steps)
     cmed, cmin, cmax = cold(fn, flush, cold_samples)
     scale = 1e9 if unit == "GB/s" else 1e12
     rate = work / (warm * 1e-3) / scale
@@ -389,18 +407,25 @@ def run_configs(dev, mod, rt, profile_calls=0):
         return res
     nramp = ramp(loop, 0.05)
     loop()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nsteps)]
-    reps, per_step = 3, np.zeros(nsteps)
+    # The rate: the 32 steps back to back between two events, three times.
+    reps, total_ms = 3, 0.0
     for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        for s, (a, b) in enumerate(ev):
-            a.record()
-            flash_attn_with_kvcache(qs[s], kc, vc, k=ks[s], v=vs[s], cache_seqlens=lens_t[s], page_table=table)
-            b.record()
+        a.record()
+        loop()
+        b.record()
         torch.cuda.synchronize()
-        per_step += [a.elapsed_time(b) for a, b in ev]
-    per_step /= reps
-    total_ms = float(per_step.sum())
+        total_ms += a.elapsed_time(b) / reps
+    # The spread over the steps: one more pass with an event pair around each step.
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nsteps)]
+    torch.cuda.synchronize()
+    for s, (a, b) in enumerate(ev):
+        a.record()
+        flash_attn_with_kvcache(qs[s], kc, vc, k=ks[s], v=vs[s], cache_seqlens=lens_t[s], page_table=table)
+        b.record()
+    torch.cuda.synchronize()
+    per_step = np.array([a.elapsed_time(b) for a, b in ev])
     rate = sum(step_bytes) / (total_ms * 1e-3) / 1e9
     # cold: the caches flushed before every step (the K/V of the other layers of a
     # real model would pass through them between two steps of this one)
@@ -675,7 +700,7 @@ def main():
         assert r is not None
 
     wall, ms, nramp = timed(step, args.steps, args.warmup)
-    call_ms = float(np.mean(ms))
+    call_ms = region_ms(ms, args.steps)
     gbs_kernel = w["bytes"] / (call_ms * 1e-3) / 1e9
     # cold: caches flushed before each sample (the 1 GiB fill leaves the caches
     # full of dirty lines, whose write-back the call then pays for)
@@ -718,13 +743,13 @@ def main():
         psteps, pwarm = max(20, args.steps // 2), args.warmup
         pwall, pms, pramp = timed(pstep, psteps, pwarm)
         flop = causal_flop(N, H, E, L, L)
-        pcall = float(np.mean(pms))
+        pcall = region_ms(pms, psteps)
         pcmed, pcmin, pcmax = cold(pstep, flush, 10)
         tf = flop / (pcall * 1e-3) / 1e12
         res["prefill"] = {
             "workload": "flash_attn_func bf16 causal N=4 L=S=4096 H=32 E=128, q/k/v strided "
                         "chunks of a fused [N*L, 3*H*E] projection",
-            "value": round(flop * len(pms) / pwall / 1e12, 2), "unit": "TFLOP/s",
+            "value": round(flop * psteps / pwall / 1e12, 2), "unit": "TFLOP/s",
             "steps": psteps, "warmup": pwarm, "clock_ramp_ms": RAMP_S * 1e3, "clock_ramp_calls": pramp,
             "us_per_call": round(pcall * 1e3, 1), "us_per_call_median": round(float(np.median(pms)) * 1e3, 1),
             "us_per_call_cold": round(pcmed * 1e3, 1),
