@@ -129,11 +129,12 @@ static int decode_entry(const ca_decode_args* a, void* stream, bool noalloc) {
     return CA_DECLINED;
   void* workspace = a->workspace;
   int64_t workspace_bytes = a->workspace_bytes;
+  int scratch_device = -1;  // noalloc: the device whose scratch this call uses
   if (noalloc) {
     workspace = nullptr;
     workspace_bytes = 0;
     if (need > 0) {
-      const int r = decode_noalloc_scratch(&workspace);
+      const int r = decode_noalloc_scratch(&workspace, &scratch_device);
       if (r != CA_OK) return r;
       workspace_bytes = CA_DECODE_NOALLOC_SCRATCH_BYTES;
     }
@@ -150,57 +151,63 @@ static int decode_entry(const ca_decode_args* a, void* stream, bool noalloc) {
   // token per sequence (each on a page of its own), the staging one for a prompt.
   const bool fused = a->k_new && !a->slots && per_seq == 1 &&
                      a->num_seqs * a->num_heads <= kFusedAppendMaxRows;
-  if (a->k_new && !fused) {
-    StoreParams sp{};
-    sp.key = static_cast<const uint32_t*>(a->k_new);
-    sp.value = static_cast<const uint32_t*>(a->v_new);
-    sp.tok_stride_w = a->kv_stride * esize(a->dtype) / 4;
-    sp.kc = static_cast<uint32_t*>(a->k_cache);
-    sp.vc = static_cast<uint32_t*>(a->v_cache);
-    sp.slots = a->slots;
-    sp.lens = a->lens;
-    sp.page_table = a->page_table;
-    sp.pt_width = a->page_table_width;
-    sp.ntok = a->num_seqs * per_seq;
-    sp.per_seq = per_seq;
-    sp.heads = a->num_heads;
-    sp.page = a->page_size;
-    sp.nblocks = a->num_blocks;
-    const int r = per_seq == 1 ? store_scatter_launch(sp, (int)words, st) : store_launch(sp, (int)words, st);
-    if (r != CA_OK) return r;
-  }
+  auto launch = [&]() -> int {
+    if (a->k_new && !fused) {
+      StoreParams sp{};
+      sp.key = static_cast<const uint32_t*>(a->k_new);
+      sp.value = static_cast<const uint32_t*>(a->v_new);
+      sp.tok_stride_w = a->kv_stride * esize(a->dtype) / 4;
+      sp.kc = static_cast<uint32_t*>(a->k_cache);
+      sp.vc = static_cast<uint32_t*>(a->v_cache);
+      sp.slots = a->slots;
+      sp.lens = a->lens;
+      sp.page_table = a->page_table;
+      sp.pt_width = a->page_table_width;
+      sp.ntok = a->num_seqs * per_seq;
+      sp.per_seq = per_seq;
+      sp.heads = a->num_heads;
+      sp.page = a->page_size;
+      sp.nblocks = a->num_blocks;
+      const int r = per_seq == 1 ? store_scatter_launch(sp, (int)words, st) : store_launch(sp, (int)words, st);
+      if (r != CA_OK) return r;
+    }
 
-  DecodeParams p{};
-  p.q = a->q;
-  p.q_stride = a->q_stride;
-  p.kc = static_cast<const uint32_t*>(a->k_cache);
-  p.vc = a->v_cache;
-  p.lens = a->lens;
-  // Appending at lens: the row attends lens + 1 keys.  With slots, lens is
-  // already the post-store length (_C.mojo:100-103, paged_attn.mojo:721-723).
-  p.len_add = (a->k_new && !a->slots) ? (int32_t)per_seq : 0;
-  p.page_table = a->page_table;
-  p.pt_width = a->page_table_width;
-  p.heads = a->num_heads;
-  p.page = a->page_size;
-  p.nblocks = a->num_blocks;
-  p.nseqs = a->num_seqs;
-  p.c = a->scale * kLog2e;
-  p.tile_keys = tile_keys;
-  p.tiles = (int)decode_tiles(a->page_table_width, a->page_size, tile_keys);
-  p.slots = decode_workspace_slots(rows, p.tiles);
-  const int64_t acc_bytes = decode_acc_bytes(p.slots, a->head_dim);
-  p.part_acc = static_cast<float*>(workspace);
-  p.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes);
-  p.out = a->out;
-  if (fused) {
-    p.k_new = static_cast<const uint32_t*>(a->k_new);
-    p.v_new = static_cast<const uint32_t*>(a->v_new);
-    p.kv_stride_w = a->kv_stride * esize(a->dtype) / 4;
-    p.kc_store = static_cast<uint32_t*>(a->k_cache);
-    p.vc_store = static_cast<uint32_t*>(a->v_cache);
-  }
-  return decode_launch(p, (int)a->head_dim, a->dtype == CA_BF16, st);
+    DecodeParams p{};
+    p.q = a->q;
+    p.q_stride = a->q_stride;
+    p.kc = static_cast<const uint32_t*>(a->k_cache);
+    p.vc = a->v_cache;
+    p.lens = a->lens;
+    // Appending at lens: the row attends lens + 1 keys.  With slots, lens is
+    // already the post-store length (_C.mojo:100-103, paged_attn.mojo:721-723).
+    p.len_add = (a->k_new && !a->slots) ? (int32_t)per_seq : 0;
+    p.page_table = a->page_table;
+    p.pt_width = a->page_table_width;
+    p.heads = a->num_heads;
+    p.page = a->page_size;
+    p.nblocks = a->num_blocks;
+    p.nseqs = a->num_seqs;
+    p.c = a->scale * kLog2e;
+    p.tile_keys = tile_keys;
+    p.tiles = (int)decode_tiles(a->page_table_width, a->page_size, tile_keys);
+    p.slots = decode_workspace_slots(rows, p.tiles);
+    const int64_t acc_bytes = decode_acc_bytes(p.slots, a->head_dim);
+    p.part_acc = static_cast<float*>(workspace);
+    p.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes);
+    p.out = a->out;
+    if (fused) {
+      p.k_new = static_cast<const uint32_t*>(a->k_new);
+      p.v_new = static_cast<const uint32_t*>(a->v_new);
+      p.kv_stride_w = a->kv_stride * esize(a->dtype) / 4;
+      p.kc_store = static_cast<uint32_t*>(a->k_cache);
+      p.vc_store = static_cast<uint32_t*>(a->v_cache);
+    }
+    return decode_launch(p, (int)a->head_dim, a->dtype == CA_BF16, st);
+  };
+  // The no-allocation entry's calls that use its one scratch buffer run one after
+  // another on the device, whichever streams they come on.
+  if (scratch_device >= 0) return decode_noalloc_ordered(scratch_device, st, launch);
+  return launch();
 }
 
 

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <functional>
+
 namespace ca {
 
 struct StoreParams {
@@ -134,7 +136,10 @@ int decode_tile_keys(int64_t rows, int64_t pt_width, int64_t page, int64_t head_
 int64_t decode_tiles(int64_t pt_width, int64_t page, int tile_keys);
 int64_t decode_workspace_slots(int64_t rows, int64_t tiles);
 int decode_launch(const DecodeParams& p, int head_dim, int bf16, hipStream_t stream);
-int decode_noalloc_scratch(void** ptr);
+// ca_decode_noalloc's scratch on the current device (and that device's index),
+// and the ordering of the calls that use it: see ca_noalloc.hip.
+int decode_noalloc_scratch(void** ptr, int* device);
+int decode_noalloc_ordered(int device, hipStream_t stream, const std::function<int()>& launch);
 // How flash_launch runs a call: the kernel, its grid (gy = splits of the keys
 // in the split modes), and whether the combine kernel merges `splits` partials
 // per row afterwards.  kind is kPlanDeclined for a call the kernels cannot take.

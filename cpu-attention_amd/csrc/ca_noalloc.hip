@@ -5,6 +5,7 @@
 // on that device.  Processes that never call ca_decode_noalloc do not reserve it;
 // those that do keep it on each GPU that ran such a call until the process ends.
 #include <atomic>
+#include <functional>
 #include <mutex>
 
 #include "ca_device.h"
@@ -22,11 +23,18 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch[kMaxDevices];
 std::mutex g_scratch_mu;
+// Per device: an event recorded after the kernels of the last call that used the
+// scratch there (none until the first such call), and the mutex that orders the
+// calls' wait-launch-record sequences.
+hipEvent_t g_last[kMaxDevices];
+bool g_has_last[kMaxDevices];
+std::mutex g_use_mu[kMaxDevices];
 }  // namespace
 
 // The current device's copy of `scratch`, looked up once per device (with that
-// device current) and remembered.
-int decode_noalloc_scratch(void** ptr) {
+// device current) and remembered, with the device's ordering event created at the
+// same set-up.
+int decode_noalloc_scratch(void** ptr, int* device) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return CA_HIP_ERROR - (int)e;
@@ -39,10 +47,39 @@ int decode_noalloc_scratch(void** ptr) {
       e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
       if (e != hipSuccess) return CA_HIP_ERROR - (int)e;
       if (!p) return CA_HIP_ERROR;
+      e = hipEventCreateWithFlags(&g_last[dev], hipEventDisableTiming);
+      if (e != hipSuccess) return CA_HIP_ERROR - (int)e;
       g_scratch[dev].store(p, std::memory_order_release);
     }
   }
   *ptr = p;
+  *device = dev;
+  return CA_OK;
+}
+
+// Runs launch(), which enqueues the kernels of one call that uses `device`'s
+// scratch on `stream`, after every earlier such call's kernels on that device:
+// the stream first waits for the event recorded after the previous call (on
+// whichever stream it ran), and the event is recorded again after this call.
+// The host mutex keeps the wait, the launch and the record of one call together.
+// A stream under graph capture neither waits nor records (an event recorded
+// outside the capture cannot be waited on inside it): captured calls, and their
+// replays, are ordered by the caller.
+int decode_noalloc_ordered(int device, hipStream_t stream, const std::function<int()>& launch) {
+  std::lock_guard<std::mutex> lock(g_use_mu[device]);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(stream, &cap);
+  if (e != hipSuccess) return CA_HIP_ERROR - (int)e;
+  const bool order = cap == hipStreamCaptureStatusNone;
+  if (order && g_has_last[device]) {
+    e = hipStreamWaitEvent(stream, g_last[device], 0);
+    if (e != hipSuccess) return CA_HIP_ERROR - (int)e;
+  }
+  const int r = launch();
+  if (r != CA_OK || !order) return r;
+  e = hipEventRecord(g_last[device], stream);
+  if (e != hipSuccess) return CA_HIP_ERROR - (int)e;
+  g_has_last[device] = true;
   return CA_OK;
 }
 

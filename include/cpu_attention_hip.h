@@ -157,11 +157,16 @@ int ca_decode(const ca_decode_args* args, void* stream);
  * do not fit, it returns CA_SCRATCH_EXCEEDED and enqueues nothing (32 MiB
  * covers, e.g., 4096 rows of E=128 up to 30,720 keys of page-table capacity).
  * Rows whose page table holds at most one block of tiles (512 keys with 64-key
- * tiles, 2048 with 256-key tiles) need no scratch.  Every call
- * on a GPU shares that GPU's one buffer: calls that overlap on one GPU (two
- * streams, or two host threads) race on it and must be serialised by the
- * caller.  The buffer needs no clearing: each call writes every partial it
- * reads before reading it. */
+ * tiles, 2048 with 256-key tiles) need no scratch.  Every call on a GPU that
+ * uses the scratch shares that GPU's one buffer, so the entry orders such calls
+ * itself: each one's kernels wait, on its stream, for an event recorded after
+ * the previous such call's kernels on that GPU (whichever stream they ran on),
+ * and host threads take turns for the wait-launch-record sequence (one event per
+ * GPU, created at the same set-up as the address lookup).  A stream under graph
+ * capture neither waits nor records: calls captured into graphs, and the graphs'
+ * replays, must be ordered by the caller against every other use of the buffer.
+ * The buffer needs no clearing: each call writes every partial it reads before
+ * reading it. */
 #define CA_DECODE_NOALLOC_SCRATCH_BYTES (32ll << 20)
 int ca_decode_noalloc(const ca_decode_args* args, void* stream);
 

@@ -3,8 +3,9 @@ is a fixed per-GPU buffer inside the library) against ca_decode with a caller
 workspace, through the C ABI: two calls in a row, the second with a smaller
 batch and page table, each bit-equal to ca_decode's output and within the
 decode gates of the float64 oracle; a call whose usual tile size needs more
-scratch than the buffer holds, on 256-key tiles; a call past the buffer's size
-even then is refused without touching the output."""
+scratch than the buffer holds, on 256-key tiles; calls on two streams without a
+host synchronisation, ordered by the entry; a call past the buffer's size even
+then is refused without touching the output."""
 
 import ctypes
 
@@ -80,6 +81,41 @@ def test_noalloc_takes_long_tiles_when_short_ones_do_not_fit(cuda, dtype):
     assert rc == K.CA_OK, lib.ca_status_string(rc)
     torch.cuda.synchronize()
     assert_close(out, reference(q, ks, vs, d ** -0.5), dtype, paged=True)
+
+
+def test_noalloc_calls_on_two_streams_run_in_turn(cuda):
+    """Calls that use the one scratch buffer, issued on two streams with no host
+    synchronisation between them (two batches whose rows span several blocks,
+    alternating), each give ca_decode's output: the entry makes every such call
+    wait for the previous one's kernels, whichever stream it ran on."""
+    lib = K.module().lib
+    h, d, page = 8, 128, 16
+    dtype = torch.bfloat16
+    jobs = []
+    for lens, seed in (([5000, 2100, 4095, 3000, 2500, 4000], 7), ([3000, 2300, 1700], 8)):
+        q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=seed, device=cuda)
+        seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
+        ws = torch.empty(lib.ca_decode_workspace_bytes(len(lens), h, d, page, bt.shape[1]),
+                         dtype=torch.uint8, device=cuda)
+        ref_out = torch.empty_like(q)
+        rc = lib.ca_decode(ctypes.byref(args_for(q, kc, vc, seqlens, bt, ref_out, ws)), stream())
+        assert rc == K.CA_OK, lib.ca_status_string(rc)
+        jobs.append((q, kc, vc, seqlens, bt, ref_out))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    outs = []
+    print("noalloc on two streams", flush=True)
+    for i in range(6):
+        j = i % 2
+        q, kc, vc, seqlens, bt, _ = jobs[j]
+        out = torch.full_like(q, float("nan"))
+        rc = lib.ca_decode_noalloc(ctypes.byref(args_for(q, kc, vc, seqlens, bt, out)), streams[j].cuda_stream)
+        assert rc == K.CA_OK, lib.ca_status_string(rc)
+        outs.append((j, out))
+    torch.cuda.synchronize()
+    for j, out in outs:
+        assert torch.equal(out.view(torch.uint8), jobs[j][5].view(torch.uint8))
 
 
 def test_noalloc_refuses_past_its_buffer(cuda):
