@@ -1374,6 +1374,7 @@ FlashPlan flash_plan(const FlashParams& p, int E, bool bf16) {
   // Row and key positions are 32-bit inside the kernels.
   if (p.seq_q >= ((int64_t)1 << 30) || p.seq_k >= ((int64_t)1 << 30)) return plan;
   if (rows_route(p.batch, p.seq_q, p.heads, bf16)) return rows_plan(p, E, bf16);
+  if (small_route(p.batch, p.seq_q, p.seq_k, p.heads, bf16)) return small_plan(p);
   // Split mode: one block per (batch, head, query block) and split of its keys,
   // then the combine of each row's partials into the output.  Otherwise one
   // block per (batch, head) and query-block pair (causal) or query block.
@@ -1396,6 +1397,7 @@ int flash_launch(const FlashParams& p, int E, int bf16, hipStream_t stream) {
   if (plan.need > 0 && (p.part_acc == nullptr || p.part_ml == nullptr || p.workspace_bytes < plan.need))
     return CA_DECLINED;
   if (plan.kind == kPlanRows || plan.kind == kPlanRowsHeads) return flash_rows_launch(p, plan, E, bf16, stream);
+  if (plan.kind == kPlanSmall) return flash_small_launch(p, plan, E, stream);
   const int64_t nb = plan.gx, splits = plan.splits;
   if (bf16) {
     if (plan.split) {

@@ -80,6 +80,20 @@ __host__ __device__ inline bool rows_route(int64_t batch, int64_t seq_q, int64_t
   if (bf16) return seq_q <= 4;
   return seq_q <= kRowsMaxLFew || (seq_q <= kRowsMaxL && batch * heads >= 256);
 }
+// bf16 calls past the few-rows route whose keys number at most kSmallMaxKeys take
+// flash_small_kernel (ca_small.hip): one wave per kSmallRows query rows, every
+// key in registers, when the call has at most kSmallMaxBlocks such row blocks.
+// Measured on MI355X against the tiled kernel (bf16, back-to-back calls):
+// N=1 L=S=128 H=16 E=64 causal 8.5 -> 4.9 us, N=1 L=S=128 H=32 E=128 11.4 -> 6.3 us,
+// N=4 (512 row blocks) 11.9 -> 8.3 us; even at 2048 row blocks (N=16) 26.5 -> 26.0
+// us, and slower at 4096 (N=8 L=512 S=128: 29.4 -> 45.5 us), where the tiled
+// kernel's 256-row passes reuse each key tile for more rows.
+constexpr int64_t kSmallMaxKeys = 128;
+constexpr int kSmallRows = 32;
+constexpr int64_t kSmallMaxBlocks = 1024;
+__host__ __device__ inline bool small_route(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, bool bf16) {
+  return bf16 && seq_k <= kSmallMaxKeys && batch * heads * ((seq_q + kSmallRows - 1) / kSmallRows) <= kSmallMaxBlocks;
+}
 constexpr int kRowsWaves = 8;                 // waves per block
 constexpr int64_t kRowsTargetBlocks = 256;    // blocks that keep every CU streaming
 constexpr int64_t kRowsMaxSplits = 64;
@@ -143,7 +157,7 @@ int decode_noalloc_ordered(int device, hipStream_t stream, const std::function<i
 // How flash_launch runs a call: the kernel, its grid (gy = splits of the keys
 // in the split modes), and whether the combine kernel merges `splits` partials
 // per row afterwards.  kind is kPlanDeclined for a call the kernels cannot take.
-enum { kPlanDeclined = 0, kPlanNone, kPlanRows, kPlanRowsHeads, kPlanBf16, kPlanF32 };
+enum { kPlanDeclined = 0, kPlanNone, kPlanRows, kPlanRowsHeads, kPlanBf16, kPlanF32, kPlanSmall };
 struct FlashPlan {
   int kind;
   int rows_r;      // kPlanRows: query rows per wave group (1 or kRowsPerWave)
@@ -164,6 +178,9 @@ void flash_rows_workspace(FlashParams& p, void* ws, int64_t bytes, int head_dim,
 int flash_rows_launch(const FlashParams& p, const FlashPlan& plan, int head_dim, int bf16, hipStream_t stream);
 // The few-rows route's part of flash_plan (p.seq_q within rows_route).
 FlashPlan rows_plan(const FlashParams& p, int head_dim, bool bf16);
+// The short-key route's plan (small_route) and launch.
+FlashPlan small_plan(const FlashParams& p);
+int flash_small_launch(const FlashParams& p, const FlashPlan& plan, int head_dim, hipStream_t stream);
 // Merges each row's `splits` partials (p.part_acc / p.part_ml) into p.out.
 int flash_combine_launch(const FlashParams& p, int head_dim, int bf16, int64_t splits, hipStream_t stream);
 

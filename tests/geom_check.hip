@@ -4,7 +4,7 @@
 // It includes the kernel sources and replays, for each call shape it reads from
 // stdin, the launcher's own plan (flash_plan: route, grid, splits) and the index
 // arithmetic the kernels themselves call (bf16_block_work / pair_work /
-// block_work / rows_work / heads_work, bf16_pass_geom, bf16_row_tiles, f32_keys,
+// block_work / rows_work / heads_work / small_work, bf16_pass_geom, bf16_row_tiles, f32_keys,
 // tile_window, window_bytes, tile_offsets, f32_tile_offset, f32_tile_bytes,
 // rows_kend).  For every block, split, pass, wave, tile, load and lane it forms
 // each global access the kernel would make (the bytes a buffer window lets
@@ -23,6 +23,9 @@
 
 #include "../cpu-attention_amd/csrc/ca_flash.hip"
 #include "../cpu-attention_amd/csrc/ca_rows.hip"
+#include "../cpu-attention_amd/csrc/ca_small.hip"
+
+#include <vector>
 
 using namespace ca;
 
@@ -233,6 +236,87 @@ static bool check_rows(const FlashParams& p, const FlashPlan& plan, const Ten& q
   return true;
 }
 
+// flash_small_kernel: one wave per (batch, head, 32 query rows); every block's
+// work must be a distinct row block, and every guarded load and output store
+// must lie inside its tensor.
+template <int E>
+static bool check_small(const FlashParams& p, const FlashPlan& plan, const Ten& q, const Ten& k, const Ten& v) {
+  const int L = (int)p.seq_q, S = (int)p.seq_k, NKB = (int)cdiv(S, 32);
+  if (NKB < 1 || NKB > 4) FAIL("small: %d key blocks", NKB);
+  const int64_t nrb = cdiv(L, kSmallRows);
+  if (plan.gx != p.batch * p.heads * nrb || plan.gy != 1) FAIL("small: grid");
+  std::vector<char> seen((size_t)plan.gx, 0);
+  const int64_t out_elems = p.batch * p.seq_q * p.heads * E;
+  for (int64_t bx = 0; bx < plan.gx; ++bx) {
+    const SmallWork w = small_work(p, bx, plan.gx);
+    if (w.b < 0 || w.b >= p.batch || w.h < 0 || w.h >= p.heads || w.r0 < 0 || w.r0 >= L || w.r0 % kSmallRows)
+      FAIL("small block %lld: bad work", (long long)bx);
+    const int64_t id = (w.b * p.heads + w.h) * nrb + w.r0 / kSmallRows;
+    if (seen[(size_t)id]++) FAIL("small: row block given to two blocks");
+    for (int lane = 0; lane < 64; ++lane) {
+      const int n = lane & 31, hf = lane >> 5, row = w.r0 + n;
+      const int64_t qrow = row < L ? row : L - 1;  // every lane loads; past L the last row
+      for (int ks = 0; ks < E / 16; ++ks) {
+        ++g_checks;
+        if (!q.inside(w.b, w.h, (w.b * q.s0 + w.h * q.s2 + qrow * q.s1 + 16 * ks + 8 * hf) * 2, 16, L))
+          FAIL("small: Q row %lld", (long long)qrow);
+      }
+      if (row < L) {
+        if (small_kend(p, row) > S) FAIL("small: row %d sees keys past S", row);
+        for (int db = 0; db < E / 32; ++db)
+          for (int i = 0; i < 4; ++i) {
+            const int64_t o = ((w.b * L + row) * p.heads + w.h) * (int64_t)E + 32 * db + small_acc_row(4 * i, hf);
+            ++g_checks;
+            if (o < 0 || o + 4 > out_elems || (o % E) + 4 > E) FAIL("small: output row %d", row);
+          }
+      }
+      // K and V: 32-bit byte offsets from the (b, h) base, keys clamped to S - 1
+      for (int kb = 0; kb < NKB; ++kb) {
+        const int64_t kkey = small_clamp_key(32 * kb + n, S);
+        for (int ks = 0; ks < E / 16; ++ks) {
+          const uint64_t off64 = (uint64_t)kkey * (uint64_t)p.ks[1] * 2u + (16 * ks + 8 * hf) * 2;
+          const uint32_t off32 = (uint32_t)kkey * (uint32_t)p.ks[1] * 2u + (16 * ks + 8 * hf) * 2;
+          if (off64 != off32) FAIL("small: K offset past 32 bits");
+          ++g_checks;
+          if (!k.inside(w.b, w.h, (w.b * k.s0 + w.h * k.s2) * 2 + (int64_t)off32, 16, S))
+            FAIL("small: K row %lld", (long long)kkey);
+        }
+      }
+      // V rows staged in LDS: 16-byte chunk c = lane + 64 i is row c / CPR (clamped
+      // for the load), column chunk c % CPR; the LDS write must lie in the array
+      constexpr int CPR = E / 8, RS = small_rsv(E) * 8;
+      const int nvl = NKB * 32 * CPR / 64;
+      for (int i = 0; i < nvl; ++i) {
+        const int c = lane + 64 * i, key = c / CPR, col = c % CPR;
+        const int64_t vk = small_clamp_key(key, S);
+        const uint64_t off64 = (uint64_t)vk * (uint64_t)p.vs[1] * 2u + col * 16;
+        const uint32_t off32 = (uint32_t)vk * (uint32_t)p.vs[1] * 2u + col * 16;
+        if (off64 != off32) FAIL("small: V offset past 32 bits");
+        ++g_checks;
+        if (!v.inside(w.b, w.h, (w.b * v.s0 + w.h * v.s2) * 2 + (int64_t)off32, 16, S))
+          FAIL("small: V row %lld", (long long)vk);
+        if (key * RS + col * 8 + 8 > NKB * 32 * RS) FAIL("small: LDS write past the staged rows");
+      }
+      // the transposed reads: rows 16 cc + 8 q + 4 hf + j / 4, columns 32 d + 16 dh + 4 (j % 4) .. +3
+      const int j = lane & 15, dh = (lane >> 4) & 1;
+      for (int cc = 0; cc < 2 * NKB; ++cc)
+        for (int q = 0; q < 2; ++q)
+          for (int d = 0; d < E / 32; ++d) {
+            const int r = 16 * cc + 8 * q + 4 * hf + (j >> 2), col = 32 * d + 16 * dh + 4 * (j & 3);
+            if (r >= NKB * 32 || col + 4 > E) FAIL("small: transposed read outside the staged rows");
+          }
+    }
+  }
+  // the P.V steps' keys: each of a 16-key step's keys once, across the two halves
+  for (int u = 0; u < 2; ++u) {
+    int mask = 0;
+    for (int hf = 0; hf < 2; ++hf)
+      for (int t = 0; t < 8; ++t) mask |= 1 << (small_pv_key(u, hf, t) - 16 * u);
+    if (mask != 0xffff) FAIL("small: P.V step %d does not cover its 16 keys once", u);
+  }
+  return true;
+}
+
 template <int E>
 static bool check_e(const FlashParams& p, bool bf16, const Ten& q, const Ten& k, const Ten& v) {
   const FlashPlan plan = flash_plan(p, E, bf16);
@@ -244,6 +328,8 @@ static bool check_e(const FlashParams& p, bool bf16, const Ten& q, const Ten& k,
       return check_bf16<E>(p, plan, q, k, v);
     case kPlanF32:
       return check_f32<E>(p, plan, q, k, v);
+    case kPlanSmall:
+      return check_small<E>(p, plan, q, k, v);
     default:
       return bf16 ? check_rows<E, true>(p, plan, q, k, v) : check_rows<E, false>(p, plan, q, k, v);
   }

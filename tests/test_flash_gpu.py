@@ -337,3 +337,51 @@ def test_split_keys_module_asks_for_workspace(cuda, dtype):
     out = mod.flash(K.runtime(), q, k, k, None, False, ws.data_ptr(), need)
     ref = attention(values(q), values(k), values(k), 128 ** -0.5, False)
     assert_close(out, ref, dtype, paged=False)
+
+
+def strided(x, layout):
+    """The same values as a view with the given layout: a chunk of a fused
+    [b, s, 3 * h * d] projection, or a head-major [b, h, s, d] tensor viewed as
+    [b, s, h, d]."""
+    b, s, h, d = x.shape
+    if layout == "fused":
+        buf = torch.zeros(b, s, 3 * h * d, dtype=x.dtype, device=x.device)
+        buf[..., h * d:2 * h * d] = x.reshape(b, s, h * d)
+        return buf[..., h * d:2 * h * d].view(b, s, h, d)
+    if layout == "bhse":
+        return x.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    return x
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("layout", ["contiguous", "fused", "bhse"])
+@pytest.mark.parametrize("b,sq,sk,h", [(1, 128, 128, 16), (2, 5, 128, 3), (1, 200, 37, 4), (3, 33, 97, 2),
+                                       (1, 64, 1, 8), (2, 31, 64, 5), (1, 96, 32, 1)])
+def test_short_key_ranges(cuda, d, causal, layout, b, sq, sk, h):
+    """bf16 calls of at most 128 keys (the short-key route: one wave per 32 query
+    rows, every key in registers): partial 32-key blocks, a single key, more rows
+    than keys (causal rows that see no key are 0), more keys than rows, partial
+    32-row blocks, and q/k/v read in place from fused or head-major views."""
+    g = torch.Generator().manual_seed(sq * 131 + sk)
+    q, k, v = (strided(torch.randn(b, n, h, d, generator=g).bfloat16().to(cuda), layout) for n in (sq, sk, sk))
+    out = flash_attn_func(q, k, v, causal=causal)
+    ref = attention(values(q), values(k), values(v), d ** -0.5, causal)
+    assert_close(out, ref, torch.bfloat16, paged=False)
+    if causal and sq > sk:
+        assert torch.count_nonzero(out[:, :sq - sk]) == 0
+
+
+@pytest.mark.parametrize("b,sq,sk,h", [(8, 128, 128, 32), (8, 129, 128, 32), (2, 32, 129, 4)])
+def test_short_key_route_edges(cuda, b, sq, sk, h):
+    """Either side of the short-key route's limits: 8 x 32 x 4 = 1024 row blocks
+    (taken), 8 x 32 x 5 = 1280 (the tiled kernel), 129 keys (the tiled kernel);
+    checked on the first and last heads."""
+    d = 64
+    g = torch.Generator().manual_seed(sq + sk)
+    q, k, v = (torch.randn(b, n, h, d, generator=g).bfloat16().to(cuda) for n in (sq, sk, sk))
+    out = flash_attn_func(q, k, v, causal=True)
+    for hh in (0, h - 1):
+        sel = slice(hh, hh + 1)
+        ref = attention(values(q[:, :, sel]), values(k[:, :, sel]), values(v[:, :, sel]), d ** -0.5, True)
+        assert_close(out[:, :, sel], ref, torch.bfloat16, paged=False)

@@ -64,6 +64,13 @@ def shapes():
                                  (3, 77, 1000, 5), (1, 12, 4096, 32), (8, 9, 2048, 32), (1, 5, 4096, 32)]:
                 for causal in (False, True):
                     out.append(line(e, bf16, causal, b, sq, sk, h))
+    # the short-key route's GPU tests: layouts, partial blocks, the route's limits
+    for b, sq, sk, h in [(1, 128, 128, 16), (2, 5, 128, 3), (1, 200, 37, 4), (3, 33, 97, 2), (1, 64, 1, 8),
+                         (2, 31, 64, 5), (1, 96, 32, 1), (8, 128, 128, 32), (8, 129, 128, 32), (2, 32, 129, 4)]:
+        for e in (32, 64, 128):
+            for causal in (False, True):
+                for lay in ("bshe", "fused", "bhse"):
+                    out.append(line(e, True, causal, b, sq, sk, h, lay))
     # BASELINE: cfg1, cfg4 (fused q/k/v) and its cross shape
     out.append(line(64, True, True, 1, 128, 128, 16))
     out.append(line(128, True, True, 4, 4096, 4096, 32, "fused"))
