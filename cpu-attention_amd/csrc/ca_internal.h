@@ -104,24 +104,38 @@ constexpr int64_t kRowsMaxSplits = 64;
 // blocks (twice that in fp32, whose kernel keeps two blocks on each CU), at least
 // kTiledMinKeys keys per split, at most kTiledMaxSplits.  Such
 // calls (few rows over long key ranges) would otherwise leave most CUs idle,
-// with a block's serial walk over every key tile the whole call's time.  bf16
-// causal calls with fewer than twice as many keys as rows do not split: the
-// causal triangle is most of their work and the unsplit blocks finish sooner
-// (N=1 L=1024 H=32 E=128: 41.1 -> 33.8 us); fp32 ones split (193 -> 301 us
-// unsplit at L=1280).  So a causal call never splits more than the non-causal
-// call of the same shapes, which the workspace query answers for.
+// with a block's serial walk over every key tile the whole call's time.  In bf16
+// (one block per CU) the split count rounds down, so the split blocks fit one
+// round of the chip: rounded up, some CUs ran two blocks each (N=1 L=S=1792 H=20
+// E=128, 140 query blocks: 2 splits 77.1 us, none 48.8 us).  The fp32 kernel
+// keeps two blocks on a CU, which share its MFMA pipes; there the count rounds
+// up, and neither rounding wins everywhere: causal L=S=1280 H=16 (160 query
+// blocks) 4 splits 109.1 us, 3 splits 136.6 us; L=100 S=4096 H=300 (300) 2 splits
+// 428.2 us, unsplit 570.7 us; but L=640 S=2048 H=24 (120) 5 splits 187.2 us, 4
+// splits 152.0 us.  bf16 calls with fewer than twice as many keys as rows do not split: if
+// causal, because the causal triangle is most of their work and the unsplit
+// blocks finish sooner (N=1 L=1024 H=32 E=128: 41.1 -> 33.8 us); if not, once they
+// have kTiledMinItemsUnsplit query blocks, because the partials (fp32 (E + 2) per
+// row and split, written and read back) cost more than the shorter walks save
+// (N=1 L=S=1024 H=32 E=128: 39.7 -> 31.3 us, L=S=1500 H=20 E=64: 34.6 -> 31.5 us),
+// while fewer query blocks leave most CUs idle (N=2 L=700 S=1200 H=8 E=64, 48
+// blocks: split 23.0 us, unsplit 26.1 us).  fp32 calls split (193 -> 301 us
+// unsplit at L=1280 causal).  So a causal call never splits more than the
+// non-causal call of the same shapes, which the workspace query answers for.
 constexpr int64_t kTiledTargetBlocks = 256;
 constexpr int64_t kTiledMinKeys = 256;
 constexpr int64_t kTiledMaxSplits = 64;
+constexpr int64_t kTiledMinItemsUnsplit = 64;
 __host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads,
                                                 bool bf16, bool causal) {
   if (rows_route(batch, seq_q, heads, bf16)) return 1;
   if (bf16 && causal && seq_k < 2 * seq_q) return 1;
   const int64_t bm = bf16 ? 256 : 128;
   const int64_t items = batch * heads * ((seq_q + bm - 1) / bm);
+  if (bf16 && seq_k < 2 * seq_q && items >= kTiledMinItemsUnsplit) return 1;
   const int64_t target = bf16 ? kTiledTargetBlocks : 2 * kTiledTargetBlocks;
   if (items <= 0 || items >= target) return 1;
-  int64_t s = (target + items - 1) / items;
+  int64_t s = bf16 ? target / items : (target + items - 1) / items;
   const int64_t by_keys = (seq_k + 63) / 64 / (kTiledMinKeys / 64);
   s = s < by_keys ? s : by_keys;
   s = s < kTiledMaxSplits ? s : kTiledMaxSplits;

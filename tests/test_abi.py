@@ -159,16 +159,21 @@ def test_flash_workspace_for_few_rows(dtype, d, chunk):
 
 
 def tiled(b, sq, sk, h, d, dtype):
-    """The tiled prefill's split mode: when its query blocks (b * h * ceil(sq /
-    rows per block): 256 in bf16, 128 in fp32) number fewer than a target (256 in
-    bf16, 512 in fp32), each one's keys are split over about target / blocks
-    blocks, at least 256 keys each (whole 64-key units) and at most 64 splits,
-    which needs (E + 2) floats per (batch, head, row, split)."""
+    """The tiled prefill's split mode (non-causal, which the workspace query
+    answers for): when its query blocks (b * h * ceil(sq / rows per block): 256 in
+    bf16, 128 in fp32) number fewer than a target (256 in bf16, 512 in fp32), each
+    one's keys are split over target / blocks blocks (rounded down in bf16: one
+    round of the chip; up in fp32), at least 256 keys each (whole
+    64-key units) and at most 64 splits,
+    which needs (E + 2) floats per (batch, head, row, split); except bf16 calls
+    with fewer than twice as many keys as rows and at least 64 query blocks, and
+    short key ranges (128 keys or fewer) in bf16, which do not split."""
     blocks = b * h * -(-sq // (256 if dtype == 1 else 128))
     target = 256 if dtype == 1 else 512
-    if blocks >= target:
+    if blocks >= target or (dtype == 1 and sk < 2 * sq and blocks >= 64):
         return 0
-    splits = min(-(-target // blocks), -(-sk // 64) // 4, 64)
+    per = target // blocks if dtype == 1 else -(-target // blocks)
+    splits = min(per, -(-sk // 64) // 4, 64)
     return 0 if splits < 2 else b * h * sq * splits * (d + 2) * 4
 
 
@@ -185,9 +190,16 @@ def test_flash_workspace_for_split_keys(d):
     for dtype in (0, 1):
         assert lib.ca_flash_workspace_bytes(4, 4096, 4096, 32, d, dtype) == 0  # cfg4: >= 2048 query blocks
         assert lib.ca_flash_workspace_bytes(1, 128, 128, 16, d, dtype) == 0  # cfg1: 128 keys
-    # 300 query blocks fill the chip in bf16 (one block per CU) but not in fp32 (two)
+    # 300 query blocks fill the chip in bf16 (one block per CU) but not in fp32 (two
+    # per CU): 2 splits
     assert lib.ca_flash_workspace_bytes(1, 100, 4096, 300, d, 1) == 0
     assert lib.ca_flash_workspace_bytes(1, 100, 4096, 300, d, 0) == 100 * 300 * 2 * (d + 2) * 4
+    # 120 query blocks: 2 splits in bf16 (256 / 120 rounded down), 5 in fp32 (512 / 120 up)
+    assert lib.ca_flash_workspace_bytes(1, 100, 4096, 120, d, 1) == 100 * 120 * 2 * (d + 2) * 4
+    assert lib.ca_flash_workspace_bytes(1, 100, 4096, 120, d, 0) == 100 * 120 * 5 * (d + 2) * 4
+    # bf16, keys under twice the rows: 64 query blocks or more do not split, fewer do
+    assert lib.ca_flash_workspace_bytes(1, 1024, 1024, 16, d, 1) == 0
+    assert lib.ca_flash_workspace_bytes(2, 700, 1200, 8, d, 1) == 2 * 8 * 700 * 4 * (d + 2) * 4
 
 
 def test_missing_library_is_a_loud_error(monkeypatch):
