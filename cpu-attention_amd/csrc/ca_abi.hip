@@ -5,6 +5,8 @@
 // anything otherwise.
 #include <stdio.h>
 
+#include <atomic>
+
 #include "ca_device.h"
 #include "ca_internal.h"
 
@@ -68,14 +70,27 @@ extern "C" int ca_store(const ca_store_args* a, void* stream) {
 }
 
 // Workspace layout: fp32 partial accumulators [slots, E], then (max, sum) pairs
-// [slots, 2], one slot per (row, block of 8 tiles of the page table's capacity).
+// [slots, 2], one slot per (row, block of 8 tiles of the page table's capacity);
+// for calls of at most kMergeMaxRows rows, then one 8-byte counter per row (the
+// in-kernel merge).
 static int64_t decode_acc_bytes(int64_t slots, int64_t head_dim) {
   return ((slots * head_dim * 4 + 255) / 256) * 256;
 }
 
+static bool decode_merges(int64_t rows, int64_t slots) { return slots > 0 && rows <= kMergeMaxRows; }
+
 static int64_t decode_ws_bytes(int64_t rows, int64_t head_dim, int64_t page, int64_t width, int tile_keys) {
   const int64_t slots = decode_workspace_slots(rows, decode_tiles(width, page, tile_keys));
-  return decode_acc_bytes(slots, head_dim) + slots * 2 * 4;
+  return decode_acc_bytes(slots, head_dim) + slots * 2 * 4 + (decode_merges(rows, slots) ? rows * 8 : 0);
+}
+
+// The in-kernel merge's per-call tag: 1, 2, ..., never 0 (the value a counter
+// holds between calls).
+static uint32_t next_merge_tag() {
+  static std::atomic<uint32_t> tag{0};
+  uint32_t t = ++tag;
+  while (t == 0) t = ++tag;
+  return t;
 }
 
 extern "C" int64_t ca_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads,
@@ -194,6 +209,10 @@ static int decode_entry(const ca_decode_args* a, void* stream, bool noalloc) {
     const int64_t acc_bytes = decode_acc_bytes(p.slots, a->head_dim);
     p.part_acc = static_cast<float*>(workspace);
     p.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes);
+    if (decode_merges(rows, p.slots)) {
+      p.counters = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + acc_bytes + p.slots * 8);
+      p.tag = next_merge_tag();
+    }
     p.out = a->out;
     if (fused) {
       p.k_new = static_cast<const uint32_t*>(a->k_new);

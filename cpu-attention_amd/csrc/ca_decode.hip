@@ -394,6 +394,22 @@ __device__ __forceinline__ float merge_states(int n, Get&& get, float& mx, float
   return l;
 }
 
+// Counts one more block of a row in: the counter word holds the call's tag (high
+// 32 bits) and the blocks counted so far (low 32).  A word with another tag (a
+// fresh workspace's contents, or 0, which the row's last block leaves behind and
+// no call uses as its tag) counts as none.  Returns the count including this
+// block.  Each failed compare-and-swap means another block's succeeded, so the
+// loop ends after at most one try per block of the row.
+__device__ __forceinline__ int merge_count_in(uint64_t* ctr, uint32_t tag) {
+  uint64_t cur = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    const uint64_t want = (uint32_t)(cur >> 32) == tag ? cur + 1 : ((uint64_t)tag << 32) | 1u;
+    if (__hip_atomic_compare_exchange_strong(ctr, &cur, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT))
+      return (int)(uint32_t)want;
+  }
+}
+
 // One wave per TK-key tile of each row, 8 tiles per block merged in LDS.
 // APPEND: the call's one-token append is done here (p.k_new).
 template <int E, bool BF, bool APPEND, int TK>
@@ -433,7 +449,7 @@ void decode_tiles_kernel(DecodeParams p) {
   }, mx, acc);
   if (blockIdx.y == 0 && len <= kDecWaves * TK) {
     if (lane * DPC < E) store_out<DPC, BF>(p.out, row * E + lane * DPC, acc, l > 0.f ? 1.f / l : 0.f);
-  } else {
+  } else if (!p.counters) {
     const int64_t slot = row * cdiv(p.tiles, kDecWaves) + blockIdx.y;
     if (lane * DPC < E) {
 #pragma unroll
@@ -443,6 +459,33 @@ void decode_tiles_kernel(DecodeParams p) {
       p.part_ml[2 * slot] = mx;
       p.part_ml[2 * slot + 1] = l;
     }
+  } else {
+    // In-kernel merge: the partial is written with agent-scope atomic stores,
+    // which the hardware makes visible device-wide (they write through the
+    // XCD's L2) by the time the wave's store counter reaches zero; only then does
+    // the block count itself in on the row's counter.  The block that completes
+    // the count has seen every other block's count, hence every other partial,
+    // and reads them with agent-scope atomic loads: no L2 write-back or
+    // invalidation, which agent-scope fences would do for the whole L2.
+    const int64_t slot = row * cdiv(p.tiles, kDecWaves) + blockIdx.y;
+    if (lane * DPC < E) {
+#pragma unroll
+      for (int i = 0; i < DPC; ++i)
+        __hip_atomic_store(p.part_acc + slot * E + lane * DPC + i, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (lane == 0) {
+      __hip_atomic_store(p.part_ml + 2 * slot, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.part_ml + 2 * slot + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const int nrow = (int)cdiv(len, (int64_t)kDecWaves * TK);
+    int arrived = 0;
+    if (lane == 0) arrived = merge_count_in(p.counters + row, p.tag);
+    arrived = __builtin_amdgcn_readfirstlane(arrived);
+    if (arrived != nrow) return;
+    asm volatile("" ::: "memory");
+    if (lane == 0) __hip_atomic_store(p.counters + row, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    merge_partials<E, BF, true>(p, row, nrow, lane);
   }
 }
 
@@ -451,21 +494,25 @@ void decode_tiles_kernel(DecodeParams p) {
 // (the kernel is latency-bound: a row has a few KB of partials); rounds merge
 // online.  A row of at most C blocks merges in one round, with the same
 // arithmetic as a single pass (weights 2^(m_t - M) against the row's max M).
-template <int E, bool BF>
-__global__ __launch_bounds__(256) void decode_tiles_combine_kernel(DecodeParams p) {
+// A partial-slot float: a plain load, or (COHERENT) a relaxed agent-scope atomic
+// load, which reads the value the device-wide coherence point holds (the in-kernel
+// merge reads partials other blocks, perhaps on other XCDs, wrote this launch).
+template <bool COHERENT>
+__device__ __forceinline__ float slot_load(float* q) {
+  if constexpr (COHERENT) return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *q;
+}
+
+// Merges row `row`'s n block partials (slots row * nb .. + n - 1) and writes the
+// row's output: one wave, lane l taking dims l * DPC ...
+template <int E, bool BF, bool COHERENT>
+__device__ __forceinline__ void merge_partials(const DecodeParams& p, int64_t row, int n, int lane) {
   constexpr int DPC = E >= 64 ? E / 64 : 1;
   constexpr int C = 8;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (row >= p.nseqs * p.heads) return;
-  const int64_t len = row_len(p, row / p.heads);
-  const int64_t span = (int64_t)kDecWaves * p.tile_keys;  // keys per block
-  if (len <= span) return;  // written by its block
   const int64_t nb = cdiv(p.tiles, kDecWaves);
-  const int n = (int)cdiv(len, span);
   const bool dims = lane * DPC < E;
-  const float* ml = p.part_ml + row * nb * 2;
-  const float* pa = p.part_acc + row * nb * E + (dims ? lane * DPC : 0);
+  float* ml = p.part_ml + row * nb * 2;
+  float* pa = p.part_acc + row * nb * E + (dims ? lane * DPC : 0);
   float m = -INFINITY, l = 0.f, acc[DPC];
 #pragma unroll
   for (int i = 0; i < DPC; ++i) acc[i] = 0.f;
@@ -474,10 +521,10 @@ __global__ __launch_bounds__(256) void decode_tiles_combine_kernel(DecodeParams 
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const bool in = t0 + c < n;
-      mt[c] = in ? ml[2 * (t0 + c)] : -INFINITY;
-      lt[c] = in ? ml[2 * (t0 + c) + 1] : 0.f;
+      mt[c] = in ? slot_load<COHERENT>(ml + 2 * (t0 + c)) : -INFINITY;
+      lt[c] = in ? slot_load<COHERENT>(ml + 2 * (t0 + c) + 1) : 0.f;
 #pragma unroll
-      for (int i = 0; i < DPC; ++i) at[c][i] = in && dims ? pa[(int64_t)(t0 + c) * E + i] : 0.f;
+      for (int i = 0; i < DPC; ++i) at[c][i] = in && dims ? slot_load<COHERENT>(pa + (int64_t)(t0 + c) * E + i) : 0.f;
     }
     float mc = m;
 #pragma unroll
@@ -497,6 +544,17 @@ __global__ __launch_bounds__(256) void decode_tiles_combine_kernel(DecodeParams 
     m = mc;
   }
   if (dims) store_out<DPC, BF>(p.out, row * E + lane * DPC, acc, l > 0.f ? 1.f / l : 0.f);
+}
+
+template <int E, bool BF>
+__global__ __launch_bounds__(256) void decode_tiles_combine_kernel(DecodeParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (row >= p.nseqs * p.heads) return;
+  const int64_t len = row_len(p, row / p.heads);
+  const int64_t span = (int64_t)kDecWaves * p.tile_keys;  // keys per block
+  if (len <= span) return;  // written by its block
+  merge_partials<E, BF, false>(p, row, (int)cdiv(len, span), lane);
 }
 
 // Tile size of a call.  64-key tiles give a row four times the waves of 256-key
@@ -548,7 +606,7 @@ static int decode_launch_t(const DecodeParams& p, hipStream_t stream) {
     append ? decode_tiles_launch<E, BF, true, kTile>(p, grid, stream)
            : decode_tiles_launch<E, BF, false, kTile>(p, grid, stream);
   int st = ca_launch_status();
-  if (st != CA_OK || gy == 1) return st;
+  if (st != CA_OK || gy == 1 || p.counters) return st;
   hipLaunchKernelGGL((decode_tiles_combine_kernel<E, BF>), dim3((unsigned)cdiv(rows, 4)), dim3(256),
                      0, stream, p);
   return ca_launch_status();

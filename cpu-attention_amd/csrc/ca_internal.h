@@ -39,6 +39,11 @@ struct DecodeParams {
   int64_t slots;          // partial slots the workspace holds
   float* part_acc;        // [slots, E]
   float* part_ml;         // [slots, 2]: running max (scaled log2 units), sum
+  // In-kernel merge (calls of at most kMergeMaxRows rows; nullptr: the combine
+  // kernel merges): one counter word per row after the partials, and the call's
+  // tag (never 0) that marks a word as this call's.
+  uint64_t* counters;
+  uint32_t tag;
   void* out;              // [N, H, E] contiguous
   // The one-token append done inside the decode (nullptr: none): token s of
   // k_new/v_new ([N, H, W] word rows, sequence stride kv_stride_w) is written to
@@ -155,6 +160,15 @@ __host__ __device__ inline int64_t tiled_workspace_bytes(int64_t batch, int64_t 
 // because the token's K words, 4 bytes in each of W lines (K is transposed in the
 // page), are partial-line writes that then compete with the decode's reads.
 constexpr int64_t kFusedAppendMaxRows = 1024;
+
+// Split rows of calls with at most this many rows are merged by their last block
+// inside the decode kernel instead of by the combine kernel.  Measured on MI355X
+// (bf16 E=128 page 16 unless noted, back-to-back calls): 32 rows 9.91 -> 9.37 us,
+// 64 rows 11.20 -> 10.38 us, 128 rows 17.89 -> 16.69 us (fp32 H=16 E=64 with an
+// append: 18.24 -> 16.96 us), 512 rows 38.0 -> 37.4 us; 1024 rows even (86.2 ->
+// 85.8 us; fp32 E=64 84.7 -> 85.6 us), 4096 rows (bf16 E=128 page 32) 189.3 ->
+// 191.4 us.
+constexpr int64_t kMergeMaxRows = 512;
 
 int store_launch(const StoreParams& p, int words, hipStream_t stream);
 // One token per sequence (p.per_seq == 1): one wave per (token, head), no staging.

@@ -112,7 +112,9 @@ def test_entries_decline_malformed_calls_without_a_gpu():
     # block of 256-key tiles (2048 keys), there are 256 rows or more, and K holds at
     # most 80 Mi elements at the page table's capacity.
     def partials(rows, blocks, d):
-        return ((rows * blocks * d * 4 + 255) // 256) * 256 + rows * blocks * 2 * 4
+        # accumulators (256-byte aligned), (max, sum) pairs, and for calls of at most
+        # 512 rows one 8-byte merge counter per row
+        return ((rows * blocks * d * 4 + 255) // 256) * 256 + rows * blocks * 2 * 4 + (rows * 8 if rows <= 512 else 0)
     assert lib.ca_decode_workspace_bytes(8, 32, 64, 32, 64) == 0          # 256-key tiles
     assert lib.ca_decode_workspace_bytes(64, 32, 128, 32, 64) == partials(2048, 4, 128)
     assert lib.ca_decode_workspace_bytes(4, 32, 64, 32, 64) == partials(128, 4, 64)  # < 256 rows

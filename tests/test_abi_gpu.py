@@ -1,9 +1,12 @@
 """C-ABI workspace rules on the GPU: a decode workspace sized once for the largest
 batch of a page table serves a smaller batch whose preferred tiles would need more
 (the entry takes 256-key tiles instead), and ca_flash declines a workspace that is
-not 16-byte aligned for a call that uses one, without touching the output."""
+not 16-byte aligned for a call that uses one, without touching the output; the
+decode's in-kernel merge of small calls works from any workspace contents."""
 
 import ctypes
+
+import numpy as np
 
 import pytest
 import torch
@@ -78,3 +81,64 @@ def test_flash_declines_a_misaligned_workspace(cuda, dtype, sq):
     assert rc == K.CA_OK, lib.ca_status_string(rc)
     torch.cuda.synchronize()
     assert_close(out, attention(values(q), values(k), values(v), d ** -0.5, False), dtype, paged=False)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_merge_counters_in_any_workspace(cuda, dtype):
+    """Calls of at most 512 rows merge their split rows inside the decode kernel:
+    each block counts itself in on a per-row counter in the workspace, tagged with
+    the call, and the row's last block merges.  Whatever the workspace holds
+    beforehand (zeros, all-ones bytes, random bytes, the previous call's counters),
+    ten calls in a row give the same bits, within the oracle's gates; a second call
+    shape on the same workspace (its slots and counters elsewhere) does too."""
+    lib = K.module().lib
+    h, d, page = 8, 128, 16
+    lens = [3000, 17, 1500, 513, 2100, 64]
+    print(f"decode merge counters dtype={dtype}", flush=True)
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=31, device=cuda)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    need = lib.ca_decode_workspace_bytes(len(lens), h, d, page, bt.shape[1])
+    assert need > 0
+    g = torch.Generator(device=cuda).manual_seed(5)
+    fills = [torch.zeros(need, dtype=torch.uint8, device=cuda),
+             torch.full((need,), 255, dtype=torch.uint8, device=cuda),
+             torch.randint(0, 256, (need,), generator=g, dtype=torch.uint8, device=cuda)]
+    outs = []
+    for ws in fills:
+        for _ in range(10):
+            out = torch.full_like(q, float("nan"))
+            rc = lib.ca_decode(ctypes.byref(args_for(q, kc, vc, seqlens, bt, out, ws)), stream())
+            assert rc == K.CA_OK, lib.ca_status_string(rc)
+            outs.append(out)
+    torch.cuda.synchronize()
+    assert_close(outs[0], reference(q, ks, vs, d ** -0.5), dtype, paged=True)
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.uint8), outs[0].view(torch.uint8))
+    lens2 = [2500, 700, 1100]
+    q2, kc2, vc2, bt2, ks2, vs2 = stage(lens2, h, d, page, dtype, seed=32, device=cuda)
+    assert lib.ca_decode_workspace_bytes(len(lens2), h, d, page, bt2.shape[1]) <= need
+    out2 = torch.full_like(q2, float("nan"))
+    rc = lib.ca_decode(ctypes.byref(args_for(q2, kc2, vc2, torch.tensor(lens2, dtype=torch.int32, device=cuda), bt2,
+                                             out2, fills[2])), stream())
+    assert rc == K.CA_OK, lib.ca_status_string(rc)
+    torch.cuda.synchronize()
+    assert_close(out2, reference(q2, ks2, vs2, d ** -0.5), dtype, paged=True)
+
+
+@pytest.mark.parametrize("nseq", [16, 17])
+def test_decode_merge_row_limit(cuda, nseq):
+    """H=32: 16 sequences (512 rows) merge inside the decode kernel, 17 (544 rows)
+    go through the combine kernel; both match the oracle."""
+    lib = K.module().lib
+    h, d, page, dtype = 32, 64, 16, torch.bfloat16
+    rng = np.random.default_rng(nseq)
+    lens = rng.integers(17, 2048, size=nseq).tolist()
+    print(f"decode merge row limit nseq={nseq}", flush=True)
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=nseq, device=cuda)
+    ws = torch.empty(lib.ca_decode_workspace_bytes(nseq, h, d, page, bt.shape[1]), dtype=torch.uint8, device=cuda)
+    out = torch.full_like(q, float("nan"))
+    rc = lib.ca_decode(ctypes.byref(args_for(q, kc, vc, torch.tensor(lens, dtype=torch.int32, device=cuda), bt, out,
+                                             ws)), stream())
+    assert rc == K.CA_OK, lib.ca_status_string(rc)
+    torch.cuda.synchronize()
+    assert_close(out, reference(q, ks, vs, d ** -0.5), dtype, paged=True)
