@@ -84,12 +84,16 @@ static int64_t decode_ws_bytes(int64_t rows, int64_t head_dim, int64_t page, int
   return decode_acc_bytes(slots, head_dim) + slots * 2 * 4 + (decode_merges(rows, slots) ? rows * 8 : 0);
 }
 
-// The in-kernel merge's per-call tag: 1, 2, ..., never 0 (the value a counter
-// holds between calls).
+// The in-kernel merge's per-call tag: n * 0x9E3779B9 for the process's n-th call
+// (an odd multiplier, so no tag repeats within 2^32 calls), skipping values
+// within 2^24 of zero: never 0 (the value a counter holds between calls), nor the
+// small integers of either sign that a reused workspace tends to hold in a
+// counter's high word.
 static uint32_t next_merge_tag() {
-  static std::atomic<uint32_t> tag{0};
-  uint32_t t = ++tag;
-  while (t == 0) t = ++tag;
+  static std::atomic<uint32_t> n{0};
+  constexpr uint32_t kNear = 1u << 24;
+  uint32_t t = 0;
+  while (t < kNear || t > ~kNear) t = ++n * 0x9E3779B9u;
   return t;
 }
 

@@ -202,6 +202,85 @@ __device__ __forceinline__ void fold_chunk(const FlashParams& p, const u32x4 (&k
   }
 }
 
+// One split's partial of a row: P.V sums, max (scaled log2 units) and sum.
+template <int E, int DPC>
+__device__ __forceinline__ void rows_put_partial(const FlashParams& p, int64_t slot, const float (&acc)[DPC], float mx,
+                                                 float l, int lane) {
+  if (lane < E / DPC) {
+#pragma unroll
+    for (int d = 0; d < DPC; ++d) p.part_acc[slot * E + lane * DPC + d] = acc[d];
+  }
+  if (lane == 0) {
+    p.part_ml[2 * slot] = mx;
+    p.part_ml[2 * slot + 1] = l;
+  }
+}
+
+// Writes row `row` (= (batch*heads + head)*seq_q + query) of the output: acc * inv.
+template <int E, int DPC, bool BF>
+__device__ __forceinline__ void rows_put_out(const FlashParams& p, int64_t row, const float (&acc)[DPC], float inv,
+                                             int lane) {
+  if (lane >= E / DPC) return;
+  const int64_t bh = row / p.seq_q, i = row - bh * p.seq_q;
+  const int64_t b = bh / p.heads, h = bh - b * p.heads;
+  const int64_t oidx = ((b * p.seq_q + i) * p.heads + h) * E + lane * DPC;
+  if constexpr (BF) {
+    uint16_t* o = static_cast<uint16_t*>(p.out) + oidx;
+#pragma unroll
+    for (int d = 0; d < DPC; ++d) o[d] = (uint16_t)pack_bf16x2(acc[d] * inv, 0.f);
+  } else {
+    float* o = static_cast<float*>(p.out) + oidx;
+#pragma unroll
+    for (int d = 0; d < DPC; ++d) o[d] = acc[d] * inv;
+  }
+}
+
+// One wave merges row `row`'s partials of all splits (at most 64) and writes the
+// row: lane t loads split t's max and sum and computes its weight; the P.V
+// partials come C splits at a time, every load of a round issued before any is
+// used (the merge is latency-bound), each weighted by its lane's weight.
+static_assert(kRowsMaxSplits <= kWave && kTiledMaxSplits <= kWave, "rows_merge_row takes a lane per split");
+template <int E, bool BF>
+__device__ __forceinline__ void rows_merge_row(const FlashParams& p, int64_t row, int splits, int lane) {
+  constexpr int DPC = E >= 64 ? E / 64 : 1;
+  constexpr int ACTIVE = E / DPC;
+  constexpr int C = 16;
+  const float* ml = p.part_ml + row * splits * 2;
+  float mt = -INFINITY, lt = 0.f;
+  if (lane < splits) {
+    mt = ml[2 * lane];
+    lt = ml[2 * lane + 1];
+  }
+  const float mx = wave_max(mt);
+  float acc[DPC];
+#pragma unroll
+  for (int d = 0; d < DPC; ++d) acc[d] = 0.f;
+  float inv = 0.f;
+  if (mx != -INFINITY) {
+    const float wgt = __builtin_amdgcn_exp2f(mt - mx);  // 0 for a split that saw nothing, and past the splits
+    const float l = wave_sum(wgt * lt);
+    const bool dims = lane < ACTIVE;
+    const float* pa = p.part_acc + row * splits * E + (dims ? lane * DPC : 0);
+    for (int t0 = 0; t0 < splits; t0 += C) {
+      float at[C][DPC];
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+#pragma unroll
+        for (int d = 0; d < DPC; ++d)
+          at[c][d] = t0 + c < splits && dims ? pa[(int64_t)(t0 + c) * E + d] : 0.f;
+      }
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), t0 + c));
+#pragma unroll
+        for (int d = 0; d < DPC; ++d) acc[d] = fmaf(w, at[c][d], acc[d]);
+      }
+    }
+    inv = l > 0.f ? 1.f / l : 0.f;
+  }
+  rows_put_out<E, DPC, BF>(p, row, acc, inv, lane);
+}
+
 // Block = kRowsWaves waves on one (batch, head, row group) and one split of its
 // chunks: wave w walks chunks sp*W + w, + W*splits, ..., with the next chunk's
 // loads in flight while it folds the current one.  The waves' states merge in
@@ -313,32 +392,11 @@ __global__ __launch_bounds__(64 * kRowsWaves) void flash_rows_kernel(FlashParams
         }
       }
     }
-    const int64_t i = i0 + r;
-    if (splits == 1) {
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-      if (lane < ACTIVE) {
-        const int64_t oidx = ((b * p.seq_q + i) * p.heads + h) * E + lane * DPC;
-        if constexpr (BF) {
-          uint16_t* o = static_cast<uint16_t*>(p.out) + oidx;
-#pragma unroll
-          for (int d = 0; d < DPC; ++d) o[d] = (uint16_t)pack_bf16x2(acc[d] * inv, 0.f);
-        } else {
-          float* o = static_cast<float*>(p.out) + oidx;
-#pragma unroll
-          for (int d = 0; d < DPC; ++d) o[d] = acc[d] * inv;
-        }
-      }
-    } else {
-      const int64_t slot = (bh * p.seq_q + i) * splits + sp;
-      if (lane < ACTIVE) {
-#pragma unroll
-        for (int d = 0; d < DPC; ++d) p.part_acc[slot * E + lane * DPC + d] = acc[d];
-      }
-      if (lane == 0) {
-        p.part_ml[2 * slot] = mx;
-        p.part_ml[2 * slot + 1] = l;
-      }
-    }
+    const int64_t row = bh * p.seq_q + i0 + r;
+    if (splits == 1)
+      rows_put_out<E, DPC, BF>(p, row, acc, l > 0.f ? 1.f / l : 0.f, lane);
+    else
+      rows_put_partial<E, DPC>(p, row * splits + sp, acc, mx, l, lane);
   }
 }
 
@@ -375,18 +433,16 @@ __host__ __device__ inline int64_t rows_heads_splits(int64_t batch, int64_t seq_
   return s < 1 ? 1 : s;
 }
 
-// The call takes flash_rows_heads_kernel: one query row, packed heads, a head
-// count the loads divide, and at most kRowsHeadsMaxKeys keys.  Measured on
-// MI355X with flushed caches against the per-head route: N=64 H=32 E=32 bf16,
-// 512 keys, 44.8 -> 29.8 us; 1024 keys (N=32 H=16) 23.0 -> 22.9 us; past that the
-// per-head route, which needs no combine pass at these batch sizes, is as fast or
-// faster (N=8 H=32 E=32, 2048 keys: 23.5 against 24.2 us).
-constexpr int64_t kRowsHeadsMaxKeys = 1024;
-__host__ __device__ inline bool rows_heads_shapes(int64_t seq_q, int64_t seq_k, int64_t heads, int E, bool bf16) {
-  return seq_q == 1 && seq_k <= kRowsHeadsMaxKeys && heads % rows_heads_per_load(E, bf16) == 0;
+// The call takes flash_rows_heads_kernel: one query row, packed heads and a head
+// count the loads divide, at any key count.  Measured on MI355X (bf16, back-to-back
+// calls) against the per-head route: N=64 H=32 E=32, 512 keys, 44.8 -> 29.8 us;
+// N=8 H=32 E=32, 2048 keys 20.5 -> 18.4 us, 4096 keys 38.0 -> 25.8 us, 8192 keys
+// 74.1 -> 45.1 us; E=64 2048 keys 29.2 -> 26.6 us; E=128 8192 keys 174.7 -> 170.6 us.
+__host__ __device__ inline bool rows_heads_shapes(int64_t seq_q, int64_t heads, int E, bool bf16) {
+  return seq_q == 1 && heads % rows_heads_per_load(E, bf16) == 0;
 }
 __host__ __device__ inline bool rows_heads_route(const FlashParams& p, int E, bool bf16) {
-  return rows_heads_shapes(p.seq_q, p.seq_k, p.heads, E, bf16) && p.qs[2] == E && p.ks[2] == E && p.vs[2] == E;
+  return rows_heads_shapes(p.seq_q, p.heads, E, bf16) && p.qs[2] == E && p.ks[2] == E && p.vs[2] == E;
 }
 
 // Block (bx of gx, split of gy) of the packed-heads kernel: batch b, heads
@@ -518,91 +574,20 @@ __global__ __launch_bounds__(64 * kRowsWaves) void flash_rows_heads_kernel(Flash
       }
     }
     const int64_t row = b * p.heads + h0 + hh;  // seq_q == 1
-    if (splits == 1) {
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-      if (lane < ACTIVE) {
-        const int64_t oidx = row * E + lane * DPC;
-        if constexpr (BF) {
-          uint16_t* o = static_cast<uint16_t*>(p.out) + oidx;
-#pragma unroll
-          for (int d = 0; d < DPC; ++d) o[d] = (uint16_t)pack_bf16x2(acc[d] * inv, 0.f);
-        } else {
-          float* o = static_cast<float*>(p.out) + oidx;
-#pragma unroll
-          for (int d = 0; d < DPC; ++d) o[d] = acc[d] * inv;
-        }
-      }
-    } else {
-      const int64_t slot = row * splits + sp;
-      if (lane < ACTIVE) {
-#pragma unroll
-        for (int d = 0; d < DPC; ++d) p.part_acc[slot * E + lane * DPC + d] = acc[d];
-      }
-      if (lane == 0) {
-        p.part_ml[2 * slot] = mx;
-        p.part_ml[2 * slot + 1] = l;
-      }
-    }
+    if (splits == 1)
+      rows_put_out<E, DPC, BF>(p, row, acc, l > 0.f ? 1.f / l : 0.f, lane);
+    else
+      rows_put_partial<E, DPC>(p, row * splits + sp, acc, mx, l, lane);
   }
 }
 
-// One wave per (batch, head, query) row: merges the row's partials of all splits.
-// The maxima come in one round (a lane per split); the P.V partials C at a time,
-// every load of a round issued before any is used (the kernel is latency-bound).
+// One wave per (batch, head, query) row: merges the row's partials of all splits
+// (the few-rows kernels' and the tiled kernel's split modes).
 template <int E, bool BF>
 __global__ __launch_bounds__(256) void flash_rows_combine_kernel(FlashParams p, int splits) {
-  constexpr int DPC = E >= 64 ? E / 64 : 1;
-  constexpr int ACTIVE = E / DPC;
-  constexpr int C = 8;
-  const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= p.batch * p.heads * p.seq_q) return;
-  const int64_t bh = row / p.seq_q, i = row - bh * p.seq_q;
-  const int64_t b = bh / p.heads, h = bh - b * p.heads;
-  const float* ml = p.part_ml + row * splits * 2;
-  float mx = -INFINITY;
-  for (int t = lane; t < splits; t += kWave) mx = fmaxf(mx, ml[2 * t]);
-  mx = wave_max(mx);
-  float acc[DPC];
-#pragma unroll
-  for (int d = 0; d < DPC; ++d) acc[d] = 0.f;
-  float inv = 0.f;
-  if (mx != -INFINITY) {
-    float l = 0.f;
-    const bool dims = lane < ACTIVE;
-    const float* pa = p.part_acc + row * splits * E + (dims ? lane * DPC : 0);
-    for (int t0 = 0; t0 < splits; t0 += C) {
-      float mt[C], lt[C], at[C][DPC];
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        const bool in = t0 + c < splits;
-        mt[c] = in ? ml[2 * (t0 + c)] : -INFINITY;
-        lt[c] = in ? ml[2 * (t0 + c) + 1] : 0.f;
-#pragma unroll
-        for (int d = 0; d < DPC; ++d) at[c][d] = in && dims ? pa[(int64_t)(t0 + c) * E + d] : 0.f;
-      }
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        const float wgt = __builtin_amdgcn_exp2f(mt[c] - mx);
-        l = fmaf(wgt, lt[c], l);
-#pragma unroll
-        for (int d = 0; d < DPC; ++d) acc[d] = fmaf(wgt, at[c][d], acc[d]);
-      }
-    }
-    inv = l > 0.f ? 1.f / l : 0.f;
-  }
-  if (lane < ACTIVE) {
-    const int64_t oidx = ((b * p.seq_q + i) * p.heads + h) * E + lane * DPC;
-    if constexpr (BF) {
-      uint16_t* o = static_cast<uint16_t*>(p.out) + oidx;
-#pragma unroll
-      for (int d = 0; d < DPC; ++d) o[d] = (uint16_t)pack_bf16x2(acc[d] * inv, 0.f);
-    } else {
-      float* o = static_cast<float*>(p.out) + oidx;
-#pragma unroll
-      for (int d = 0; d < DPC; ++d) o[d] = acc[d] * inv;
-    }
-  }
+  rows_merge_row<E, BF>(p, row, splits, threadIdx.x & 63);
 }
 
 // Splits of each row group's chunks across blocks: one unless the row groups
@@ -623,6 +608,12 @@ static int64_t rows_call_splits(const FlashParams& p, int E, bool bf16) {
                                       : rows_splits(p.batch, p.seq_q, p.seq_k, p.heads, E, bf16);
 }
 
+// Bytes of the few-rows route's workspace at `splits`: the partials, E + 2 floats
+// each.
+__host__ __device__ inline int64_t rows_ws_bytes(int64_t rows, int64_t splits, int E) {
+  return splits > 1 ? rows * splits * (E + 2) * 4 : 0;
+}
+
 // The workspace a call of these shapes may need: its strides are not known
 // here, so the larger of the two routes' partials; past the few-rows route, the
 // tiled kernel's split mode.
@@ -630,12 +621,11 @@ int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, 
                                    bool bf16) {
   if (!rows_route(batch, seq_q, heads, bf16)) return tiled_workspace_bytes(batch, seq_q, seq_k, heads, E, bf16, false);
   int64_t splits = rows_splits(batch, seq_q, seq_k, heads, E, bf16);
-  if (rows_heads_shapes(seq_q, seq_k, heads, E, bf16)) {
+  if (rows_heads_shapes(seq_q, heads, E, bf16)) {
     const int64_t hs = rows_heads_splits(batch, seq_k, heads, E, bf16);
     splits = splits > hs ? splits : hs;
   }
-  if (splits <= 1) return 0;
-  return batch * heads * seq_q * splits * (E + 2) * 4;
+  return rows_ws_bytes(batch * heads * seq_q, splits, E);
 }
 
 int64_t flash_call_splits(const FlashParams& p, int E, bool bf16) {
@@ -674,7 +664,7 @@ static int rows_launch_t(const FlashParams& p, const FlashPlan& plan, hipStream_
 
 int flash_combine_launch(const FlashParams& p, int E, int bf16, int64_t splits, hipStream_t stream) {
   const int64_t rows = p.batch * p.heads * p.seq_q;
-  if (cdiv(rows, 4) > 0x7fffffff) return CA_DECLINED;
+  if (cdiv(rows, 4) > 0x7fffffff || splits > kWave) return CA_DECLINED;
   const dim3 grid((unsigned)cdiv(rows, 4));
   if (bf16) {
     switch (E) {
@@ -701,7 +691,7 @@ FlashPlan rows_plan(const FlashParams& p, int E, bool bf16) {
   plan.rows_r = rows_per_wave(p.seq_q);
   plan.gx = heads ? p.batch * (p.heads / rows_heads_per_load(E, bf16)) : p.batch * p.heads * cdiv(p.seq_q, plan.rows_r);
   plan.gy = plan.splits = rows_call_splits(p, E, bf16);
-  plan.need = plan.splits > 1 ? p.batch * p.heads * p.seq_q * plan.splits * (E + 2) * 4 : 0;
+  plan.need = rows_ws_bytes(p.batch * p.heads * p.seq_q, plan.splits, E);
   if (plan.gx > 0x7fffffff || plan.gy > 0xffff) plan.kind = kPlanDeclined;
   return plan;
 }

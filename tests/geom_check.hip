@@ -185,9 +185,27 @@ static bool check_f32(const FlashParams& p, const FlashPlan& plan, const Ten& q,
   return true;
 }
 
+// A split call's partials: they fit the workspace the plan asks for, and the grid
+// writes every (row, split) slot exactly once, so the combine kernel merges no
+// slot that a block left unwritten.
+static bool check_slots(const FlashPlan& plan, int E, int64_t rows, const std::vector<int>& written) {
+  if (plan.splits <= 1) return true;
+  if (plan.need < rows * plan.splits * (E + 2) * 4) FAIL("partials outside the workspace");
+  for (int64_t f = 0; f < (int64_t)written.size(); ++f) {
+    ++g_checks;
+    if (written[f] != 1)
+      FAIL("partial of row %lld split %lld written %d times", (long long)(f / plan.splits),
+           (long long)(f % plan.splits), written[f]);
+  }
+  return true;
+}
+
 template <int E, bool BF>
 static bool check_rows(const FlashParams& p, const FlashPlan& plan, const Ten& q, const Ten& k, const Ten& v) {
   const int esz = BF ? 2 : 4;
+  const int64_t rows = p.batch * p.heads * p.seq_q;
+  // times each (row, split) partial slot is written
+  std::vector<int> written(plan.splits > 1 ? rows * plan.splits : 0, 0);
   if (plan.kind == kPlanRowsHeads) {
     constexpr int HP = HeadsShape<E, BF>::HP, G = HeadsShape<E, BF>::G, DPL = HeadsShape<E, BF>::DPL;
     for (int64_t bx = 0; bx < plan.gx; ++bx)
@@ -202,8 +220,16 @@ static bool check_rows(const FlashParams& p, const FlashPlan& plan, const Ten& q
           if (!k.inside(hw.b, h, (hw.b * k.s0 + h * k.s2 + (p.seq_k - 1) * k.s1 + e0) * esz, 16, p.seq_k))
             FAIL("heads: last key");
         }
+        // partial slots and merged rows: rows b*heads + h0 + hh, hh < HP
+        if (plan.splits > 1) {
+          for (int hh = 0; hh < HP; ++hh) {
+            const int64_t slot = (hw.b * p.heads + hw.h0 + hh) * plan.splits + by;
+            if (slot >= rows * plan.splits) FAIL("heads: partial slot");
+            ++written[slot];
+          }
+        }
       }
-    return true;
+    return check_slots(plan, E, rows, written);
   }
   const int R = plan.rows_r;
   constexpr int CH = RowsShape<E, BF, 1>::CH, G = RowsShape<E, BF, 1>::G, DPL = RowsShape<E, BF, 1>::DPL;
@@ -222,9 +248,11 @@ static bool check_rows(const FlashParams& p, const FlashPlan& plan, const Ten& q
           if (!q.inside(rw.b, rw.h, (rw.b * q.s0 + rw.h * q.s2 + i * q.s1 + sl * DPL) * esz, 16, p.seq_q))
             FAIL("rows: q row %lld", (long long)i);
         }
-        if (plan.splits > 1 && ((rw.b * p.heads + rw.h) * p.seq_q + i) * plan.splits + by >=
-                                   p.batch * p.heads * p.seq_q * plan.splits)
-          FAIL("rows: partial slot");
+        if (plan.splits > 1) {
+          const int64_t slot = ((rw.b * p.heads + rw.h) * p.seq_q + i) * plan.splits + by;
+          if (slot >= rows * plan.splits) FAIL("rows: partial slot");
+          ++written[slot];
+        }
       }
       // the last key any lane loads (guarded by j < kend_g)
       if (rw.kend_g > 0) {
@@ -233,7 +261,7 @@ static bool check_rows(const FlashParams& p, const FlashPlan& plan, const Ten& q
           FAIL("rows: last key");
       }
     }
-  return true;
+  return check_slots(plan, E, rows, written);
 }
 
 // flash_small_kernel: one wave per (batch, head, 32 query rows); every block's

@@ -137,23 +137,36 @@ def test_flash_workspace_for_few_rows(dtype, d, chunk):
     (batch, head, row group: 1 row for single-row calls, else 4); chunks of 4 load
     steps (16-byte slices, 64 lanes).  Only when those blocks number fewer than 256
     are a row group's chunks split over more blocks (at most one chunk per wave and
-    64 splits), which needs (E + 2) floats per (batch, head, row, split);
-    otherwise no workspace."""
+    64 splits).  Single-row calls whose head count is a multiple of the heads one
+    load instruction reads (64 lanes / (E * esize / 16)) may instead take blocks of
+    one (batch, group of those heads), split the same way over chunks of 4 keys;
+    the strides choose, so the query answers for the larger.  A split call needs
+    (E + 2) floats per (batch, head, row, split); otherwise no workspace."""
     lib = K.load_library()
+
+    def split(blocks, chunks):
+        s = 1 if blocks >= 256 else -(-256 // blocks)
+        return max(1, min(s, -(-chunks // 8), 64))
 
     def expect(b, sq, sk, h):
         if sq > (4 if dtype == 1 else 16 if b * h >= 256 else 8):
             return tiled(b, sq, sk, h, d, dtype)
-        blocks = b * h * -(-sq // (1 if sq == 1 else 4))
-        splits = 1 if blocks >= 256 else -(-256 // blocks)
-        splits = max(1, min(splits, -(-(-(-sk // chunk)) // 8), 64))
-        return 0 if splits == 1 else b * h * sq * splits * (d + 2) * 4
+        splits = split(b * h * -(-sq // (1 if sq == 1 else 4)), -(-sk // chunk))
+        hp = 64 // (d * (2 if dtype == 1 else 4) // 16)
+        if sq == 1 and h % hp == 0:
+            splits = max(splits, split(b * h // hp, -(-sk // 4)))
+        rows = b * h * sq
+        return 0 if splits == 1 else rows * splits * (d + 2) * 4
 
     for b, sq, sk, h in ((1, 1, 100000, 1), (2, 16, 1000, 3), (3, 4, chunk + 1, 5), (8, 1, 2048, 32),
-                         (1, 3, 70000, 2)):
+                         (8, 1, 2048, 33), (64, 1, 512, 32), (1, 3, 70000, 2)):
         assert lib.ca_flash_workspace_bytes(b, sq, sk, h, d, dtype) == expect(b, sq, sk, h)
-    assert lib.ca_flash_workspace_bytes(1, 1, 100000, 1, d, dtype) == 1 * 1 * 1 * 64 * (d + 2) * 4
-    assert lib.ca_flash_workspace_bytes(8, 1, 2048, 32, d, dtype) == 0  # 256 blocks fill the chip
+    assert lib.ca_flash_workspace_bytes(1, 1, 100000, 1, d, dtype) == 64 * (d + 2) * 4
+    assert lib.ca_flash_workspace_bytes(8, 1, 2048, 33, d, dtype) == 0  # 264 blocks fill the chip
+    # 32 heads: the packed-heads blocks (8 x 32 / hp of them) split 2048 keys
+    hp = 64 // (d * (2 if dtype == 1 else 4) // 16)
+    s = min(-(-256 // (8 * 32 // hp)), 64)
+    assert lib.ca_flash_workspace_bytes(8, 1, 2048, 32, d, dtype) == 256 * s * (d + 2) * 4
     assert lib.ca_flash_workspace_bytes(3, 4, 8 * chunk, 5, d, dtype) == 0  # one chunk per wave
     assert lib.ca_flash_workspace_bytes(3, 17, 5000, 5, d, dtype) == tiled(3, 17, 5000, 5, d, dtype)
     assert lib.ca_flash_workspace_bytes(1, 5, 50000, 1, d, dtype) > 0  # bf16: tiled split; fp32: few rows

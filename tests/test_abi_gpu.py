@@ -88,9 +88,10 @@ def test_decode_merge_counters_in_any_workspace(cuda, dtype):
     """Calls of at most 512 rows merge their split rows inside the decode kernel:
     each block counts itself in on a per-row counter in the workspace, tagged with
     the call, and the row's last block merges.  Whatever the workspace holds
-    beforehand (zeros, all-ones bytes, random bytes, the previous call's counters),
-    ten calls in a row give the same bits, within the oracle's gates; a second call
-    shape on the same workspace (its slots and counters elsewhere) does too."""
+    beforehand (zeros, all-ones bytes, random bytes, small integers, the previous
+    call's counters), ten calls in a row give the same bits, within the oracle's
+    gates; a second call shape on the same workspace (its slots and counters
+    elsewhere) does too."""
     lib = K.module().lib
     h, d, page = 8, 128, 16
     lens = [3000, 17, 1500, 513, 2100, 64]
@@ -100,9 +101,11 @@ def test_decode_merge_counters_in_any_workspace(cuda, dtype):
     need = lib.ca_decode_workspace_bytes(len(lens), h, d, page, bt.shape[1])
     assert need > 0
     g = torch.Generator(device=cuda).manual_seed(5)
+    small = (torch.arange(need // 4, dtype=torch.int32, device=cuda) % 1000 + 1).view(torch.uint8)
     fills = [torch.zeros(need, dtype=torch.uint8, device=cuda),
              torch.full((need,), 255, dtype=torch.uint8, device=cuda),
-             torch.randint(0, 256, (need,), generator=g, dtype=torch.uint8, device=cuda)]
+             torch.randint(0, 256, (need,), generator=g, dtype=torch.uint8, device=cuda),
+             small]
     outs = []
     for ws in fills:
         for _ in range(10):

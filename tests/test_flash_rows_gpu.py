@@ -78,13 +78,13 @@ def heads_per_load(d, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("d", [32, 64, 128])
-@pytest.mark.parametrize("sk", [1, 5, 64, 300, 1024, 1025, 2049])
+@pytest.mark.parametrize("sk", [1, 5, 64, 300, 1024, 1025, 2049, 8191])
 def test_single_row_packed_heads(cuda, dtype, d, sk):
     """One query row with the heads side by side (head stride d) and a head count
-    that is a multiple of the heads per load: up to 1024 keys the route that reads
-    each key's heads as one run, with the keys split over blocks and merged by the
-    combine kernel, past that the per-head route; also with k/v as chunks of a
-    fused projection (still packed heads)."""
+    that is a multiple of the heads per load: the route that reads each key's
+    heads as one run, with the keys split over blocks and merged by each group's
+    last block; also with k/v as chunks of a fused projection (still packed
+    heads)."""
     h = 2 * heads_per_load(d, dtype)
     run(3, 1, sk, h, d, dtype, False, seed=sk + d, device=cuda)
     g = torch.Generator().manual_seed(sk)

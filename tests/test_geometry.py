@@ -71,6 +71,13 @@ def shapes():
             for causal in (False, True):
                 for lay in ("bshe", "fused", "bhse"):
                     out.append(line(e, True, causal, b, sq, sk, h, lay))
+    # single-row calls on the packed-heads route (split keys, merge counters)
+    for b, sq, sk, h in [(8, 1, 2048, 32), (8, 1, 8192, 32), (2, 1, 16384, 16), (32, 1, 2048, 32), (64, 1, 512, 32),
+                         (1, 1, 100000, 16), (3, 1, 77, 8)]:
+        for e in (32, 64, 128):
+            for bf16 in (False, True):
+                for lay in ("bshe", "fused"):
+                    out.append(line(e, bf16, False, b, sq, sk, h, lay))
     # BASELINE: cfg1, cfg4 (fused q/k/v) and its cross shape
     out.append(line(64, True, True, 1, 128, 128, 16))
     out.append(line(128, True, True, 4, 4096, 4096, 32, "fused"))
