@@ -14,7 +14,7 @@
 //
 // Work split.  A block of 8 waves takes one (batch, head, group of R query rows)
 // (R = 1 for single-row calls, else 4) and walks that group's key chunks: wave w
-// takes chunks w, w + 8, ..., with the next chunks' loads in flight (a ring of 4
+// takes chunks w, w + 8, ..., with the next chunks' loads in flight (a ring of 3
 // chunk buffers for R = 1, 2 otherwise) while it folds the current one into a
 // per-lane online softmax.  Lanes cut each K/V row into 16-byte slices: G lanes
 // per key, 64/G keys per load instruction, so every load instruction reads whole
@@ -37,7 +37,7 @@ struct RowsShape {
   static constexpr int NSTEP = 4;          // load instructions per chunk (K and V each)
   static constexpr int CH = NSTEP * KPI;   // keys per chunk
   static constexpr int R = R_;             // query rows per wave
-  static constexpr int NBUF = R == 1 ? 4 : 2;  // chunks in flight per wave
+  static constexpr int NBUF = R == 1 ? 3 : 2;  // chunks in flight per wave
 };
 
 constexpr int kRowsLoadSteps = 4;  // RowsShape::NSTEP
@@ -418,7 +418,7 @@ struct HeadsShape {
   static constexpr int G = E / DPL;        // lanes per head
   static constexpr int HP = kWave / G;     // heads per load instruction
   static constexpr int NSTEP = 4;          // keys per chunk (one load instruction each for K and V)
-  static constexpr int NBUF = 4;           // chunks in flight per wave
+  static constexpr int NBUF = 3;           // chunks in flight per wave (4 and 2 measured slower)
 };
 
 __host__ __device__ inline int rows_heads_per_load(int E, bool bf16) { return kWave / (E / (bf16 ? 8 : 4)); }
