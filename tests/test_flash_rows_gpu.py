@@ -82,9 +82,8 @@ def heads_per_load(d, dtype):
 def test_single_row_packed_heads(cuda, dtype, d, sk):
     """One query row with the heads side by side (head stride d) and a head count
     that is a multiple of the heads per load: the route that reads each key's
-    heads as one run, with the keys split over blocks and merged by each group's
-    last block; also with k/v as chunks of a fused projection (still packed
-    heads)."""
+    heads as one run, with the keys split over blocks and merged by the combine
+    kernel; also with k/v as chunks of a fused projection (still packed heads)."""
     h = 2 * heads_per_load(d, dtype)
     run(3, 1, sk, h, d, dtype, False, seed=sk + d, device=cuda)
     g = torch.Generator().manual_seed(sk)
@@ -93,6 +92,29 @@ def test_single_row_packed_heads(cuda, dtype, d, sk):
     q = torch.randn(2, 1, h, d, generator=g).to(dtype).to(cuda)
     out = flash_attn_func(q, k, v, causal=True)
     assert_close(out, attention(values(q), values(k), values(v), d ** -0.5, True), dtype, paged=False)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [32, 128])
+@pytest.mark.parametrize("packed", [True, False])
+def test_most_splits(cuda, dtype, d, packed):
+    """One (batch, head group) over 40000 keys: its keys split over 64 blocks, the
+    most there are, so the combine gives every lane of its wave a split (weights
+    read across the lanes).  Packed: one group of heads per load on the
+    packed-heads route; unpacked: one head on the per-head route, and 3 rows in
+    one group."""
+    sk = 40000
+    h = heads_per_load(d, dtype) if packed else 1
+    lib = K.load_library()
+    if packed:
+        need = lib.ca_flash_workspace_bytes(1, 1, sk, h, d, K.DTYPES[dtype])
+        assert need == h * 64 * (d + 2) * 4  # 64 splits
+        run(1, 1, sk, h, d, dtype, False, seed=d + 1, device=cuda)
+    else:
+        need = lib.ca_flash_workspace_bytes(1, 3, sk, 1, d, K.DTYPES[dtype])
+        assert need == 3 * 64 * (d + 2) * 4
+        run(1, 3, sk, 1, d, dtype, False, seed=d + 2, device=cuda)
+        run(1, 1, sk, 1, d, dtype, True, seed=d + 3, device=cuda)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
