@@ -808,7 +808,11 @@ struct P64Rows {
       for (int k = 0; k < 32 / RPI; ++k) {
         const int rr = rr0 + RPI * k, row = r0 + 32 * cb + rr;
         const u32x4 v = *reinterpret_cast<const u32x4*>(stage + rr * kStageRow + ch * 16);
-        if (row < a.L) *reinterpret_cast<u32x4*>(a.out + (int64_t)row * a.heads * E + ch * 8) = v;
+        // Non-temporal: the output is not read again here, and keeping it out of
+        // L2 leaves the lines to the K/V tiles other blocks re-read (cfg4 541 ->
+        // 534 us, N=16 L=S=1024 222 -> 212 us, bit-identical).
+        if (row < a.L)
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(a.out + (int64_t)row * a.heads * E + ch * 8));
       }
     }
   }
