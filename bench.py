@@ -86,8 +86,8 @@ METRIC = "decode HBM GB/s + µs/call; prefill TFLOP/s (bf16) vs MI355X roofline"
 TRAFFIC = {
     "decode": {"fetch_kib": 543080.5 + 1310.5, "write_kib": 2630.3 + 400.0,
                "copy_fetch_kib": 524307.9, "copy_write_kib": 1048576.0},
-    "prefill": {"fetch_kib": 295097.5, "write_kib": 132096.0,
-                "copy_fetch_kib": 524308.3, "copy_write_kib": 1048576.0},
+    "prefill": {"fetch_kib": 294720.0, "write_kib": 132097.8,
+                "copy_fetch_kib": 524315.2, "copy_write_kib": 1048576.0},
 }
 
 # The reference's published CPU figures (medians at its Python API, L2/L3 flushed,
