@@ -181,12 +181,14 @@ def test_prompt_append_replays(cuda, dtype, no_host_checks):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("sq,sk", [(300, 300), (3, 3000), (64, 3000)])
+@pytest.mark.parametrize("sq,sk", [(300, 300), (3, 3000), (1, 5000), (64, 3000)])
 def test_flash_attn_func_replays(cuda, dtype, sq, sk):
-    """Prefill: the tiled route, the few-rows route and the tiled route's split
-    mode (64 rows over 3000 keys: 11 splits and the combine kernel), whose split-K
-    scratch is allocated inside the capture from the graph's own pool."""
-    b, h, d = 2, 4, 64
+    """Prefill: the tiled route, the few-rows route (per-head, and for one query
+    row of 16 side-by-side heads the packed-heads kernel, both with split keys and
+    the combine kernel) and the tiled route's split mode (64 rows over 3000 keys:
+    11 splits and the combine kernel), whose split-K scratch is allocated inside
+    the capture from the graph's own pool."""
+    b, h, d = 2, (16 if sq == 1 else 4), 64
     q, k, v = (torch.zeros(b, n, h, d, dtype=dtype, device=cuda) for n in (sq, sk, sk))
     graph, out = capture(lambda: flash_attn_func(q, k, v, causal=True))
     g = torch.Generator(device=cuda).manual_seed(9)
