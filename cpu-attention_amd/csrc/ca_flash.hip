@@ -1378,7 +1378,10 @@ FlashPlan flash_plan(const FlashParams& p, int E, bool bf16) {
   // Row and key positions are 32-bit inside the kernels.
   if (p.seq_q >= ((int64_t)1 << 30) || p.seq_k >= ((int64_t)1 << 30)) return plan;
   if (rows_route(p.batch, p.seq_q, p.heads, bf16)) return rows_plan(p, E, bf16);
-  if (small_route(p.batch, p.seq_q, p.seq_k, p.heads, bf16)) return small_plan(p);
+  // The short-key kernel addresses K and V rows by 32-bit byte offsets from the
+  // (batch, head) base: seq_k rows of the token stride must fit (64 do, above).
+  if (small_route(p.batch, p.seq_q, p.seq_k, p.heads, E, bf16) && p.seq_k * (ts + E) * esz < ((int64_t)1 << 32))
+    return small_plan(p);
   // Split mode: one block per (batch, head, query block) and split of its keys,
   // then the combine of each row's partials into the output.  Otherwise one
   // block per (batch, head) and query-block pair (causal) or query block.

@@ -85,9 +85,10 @@ __host__ __device__ inline bool rows_route(int64_t batch, int64_t seq_q, int64_t
   if (bf16) return seq_q <= 4;
   return seq_q <= kRowsMaxLFew || (seq_q <= kRowsMaxL && batch * heads >= 256);
 }
-// bf16 calls past the few-rows route whose keys number at most kSmallMaxKeys take
-// flash_small_kernel (ca_small.hip): one wave per kSmallRows query rows, every
-// key in registers, when the call has at most kSmallMaxBlocks such row blocks.
+// bf16 calls past the few-rows route whose keys number at most small_max_keys(E)
+// (kSmallMaxKeys; twice that for head dims up to 64) take flash_small_kernel
+// (ca_small.hip): one wave per kSmallRows query rows, every key in registers, when
+// the call has at most kSmallMaxBlocks such row blocks.
 // Measured on MI355X against the tiled kernel (bf16, back-to-back calls):
 // N=1 L=S=128 H=16 E=64 causal 8.5 -> 4.9 us, N=1 L=S=128 H=32 E=128 11.4 -> 6.3 us,
 // N=4 (512 row blocks) 11.9 -> 8.3 us; even at 2048 row blocks (N=16) 26.5 -> 26.0
@@ -96,8 +97,18 @@ __host__ __device__ inline bool rows_route(int64_t batch, int64_t seq_q, int64_t
 constexpr int64_t kSmallMaxKeys = 128;
 constexpr int kSmallRows = 32;
 constexpr int64_t kSmallMaxBlocks = 1024;
-__host__ __device__ inline bool small_route(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, bool bf16) {
-  return bf16 && seq_k <= kSmallMaxKeys && batch * heads * ((seq_q + kSmallRows - 1) / kSmallRows) <= kSmallMaxBlocks;
+__host__ __device__ inline int64_t small_max_keys(int E) { return E <= 64 ? 2 * kSmallMaxKeys : kSmallMaxKeys; }
+// Row blocks that run at once: one wave per SIMD (4 per CU) on 256 CUs, except
+// that at E = 64 past 192 keys the staged V rows (42-48 KB of LDS per block) let
+// only 3 blocks share a CU.  A call that needed a second round measured slower
+// than the tiled kernel (N=4 L=S=256 H=32 E=64 causal: 12.3 against 17.6 us).
+__host__ __device__ inline int64_t small_max_blocks(int64_t seq_k, int E) {
+  return E == 64 && seq_k > 192 ? 3 * 256 : kSmallMaxBlocks;
+}
+__host__ __device__ inline bool small_route(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, int E,
+                                            bool bf16) {
+  return bf16 && seq_k <= small_max_keys(E) &&
+         batch * heads * ((seq_q + kSmallRows - 1) / kSmallRows) <= small_max_blocks(seq_k, E);
 }
 constexpr int kRowsWaves = 8;                 // waves per block
 constexpr int64_t kRowsTargetBlocks = 256;    // blocks that keep every CU streaming

@@ -1,4 +1,5 @@
-// Dense bf16 prefill over short key ranges (at most kSmallMaxKeys keys): the
+// Dense bf16 prefill over short key ranges (at most small_max_keys(E) keys: 256
+// for head dims up to 64, else 128): the
 // reference's flash_attn_func (flash_attn.mojo:127-183) for calls such as a short
 // prompt, where every key fits in registers.  The tiled kernel would spend such a
 // call on its per-pass pipeline (first-tile waits, the first softmax, the last
@@ -102,8 +103,8 @@ __global__ __launch_bounds__(64) void flash_small_kernel(FlashParams p) {
   // first wait: rows past the tensor's read its last row instead (row L - 1 for
   // Q, whose results are never stored; key S - 1 for K, whose logits are masked,
   // and for V, whose values are replaced by zeros).  K and V rows are addressed
-  // by 32-bit byte offsets from the (batch, head) base: the plan keeps 64 token
-  // strides under 2^31 bytes, so 128 do not pass 2^32.
+  // by 32-bit byte offsets from the (batch, head) base: the plan keeps seq_k
+  // token strides under 2^32 bytes.
   // Q^T operand: row `row`, dims 16 ks + 8 hf .. +7.
   const int64_t qrow = live ? row : L - 1;
   bf16x8 qo[NKS];
@@ -205,6 +206,10 @@ static int small_launch_t(const FlashParams& p, const FlashPlan& plan, hipStream
     case 2: hipLaunchKernelGGL((flash_small_kernel<E, 2>), grid, block, 0, stream, p); break;
     case 3: hipLaunchKernelGGL((flash_small_kernel<E, 3>), grid, block, 0, stream, p); break;
     case 4: hipLaunchKernelGGL((flash_small_kernel<E, 4>), grid, block, 0, stream, p); break;
+    case 5: if constexpr (E <= 64) { hipLaunchKernelGGL((flash_small_kernel<E, 5>), grid, block, 0, stream, p); break; } return CA_DECLINED;
+    case 6: if constexpr (E <= 64) { hipLaunchKernelGGL((flash_small_kernel<E, 6>), grid, block, 0, stream, p); break; } return CA_DECLINED;
+    case 7: if constexpr (E <= 64) { hipLaunchKernelGGL((flash_small_kernel<E, 7>), grid, block, 0, stream, p); break; } return CA_DECLINED;
+    case 8: if constexpr (E <= 64) { hipLaunchKernelGGL((flash_small_kernel<E, 8>), grid, block, 0, stream, p); break; } return CA_DECLINED;
     default: return CA_DECLINED;
   }
   return ca_launch_status();

@@ -71,6 +71,18 @@ def shapes():
             for causal in (False, True):
                 for lay in ("bshe", "fused", "bhse"):
                     out.append(line(e, True, causal, b, sq, sk, h, lay))
+    # the short-key route past 128 keys (head dims up to 64; E = 128 goes tiled)
+    for b, sq, sk, h in [(1, 256, 256, 16), (8, 256, 256, 16), (2, 129, 129, 3), (1, 200, 255, 4), (3, 37, 193, 2),
+                         (4, 512, 256, 8)]:
+        for e in (32, 64, 128):
+            for causal in (False, True):
+                for lay in ("bshe", "fused", "bhse"):
+                    out.append(line(e, True, causal, b, sq, sk, h, lay))
+    # a token stride whose 256 rows pass 2^32 bytes (64 rows stay under 2^31): the
+    # short-key route's 32-bit offsets do not fit, so the call goes tiled
+    big = 12 << 20
+    out.append(" ".join(str(x) for x in (64, 1, 1, 1, 200, 200, 2, 200 * big, big, 64, 200 * big, big, 64,
+                                          200 * big, big, 64)))
     # single-row calls on the packed-heads route (split keys, merge counters)
     for b, sq, sk, h in [(8, 1, 2048, 32), (8, 1, 8192, 32), (2, 1, 16384, 16), (32, 1, 2048, 32), (64, 1, 512, 32),
                          (1, 1, 100000, 16), (3, 1, 77, 8)]:
