@@ -85,29 +85,38 @@ __host__ __device__ inline bool rows_route(int64_t batch, int64_t seq_q, int64_t
   if (bf16) return seq_q <= 4;
   return seq_q <= kRowsMaxLFew || (seq_q <= kRowsMaxL && batch * heads >= 256);
 }
-// bf16 calls past the few-rows route whose keys number at most small_max_keys(E)
-// (kSmallMaxKeys; twice that for head dims up to 64) take flash_small_kernel
-// (ca_small.hip): one wave per kSmallRows query rows, every key in registers, when
-// the call has at most kSmallMaxBlocks such row blocks.
-// Measured on MI355X against the tiled kernel (bf16, back-to-back calls):
+// bf16 calls past the few-rows route whose keys number at most kSmallMaxKeys take
+// flash_small_kernel (ca_small.hip): one wave per kSmallRows query rows, every key
+// in registers, when the call's row blocks (at most kSmallMaxBlocks) all run at
+// once (small_max_blocks).  Measured on MI355X against the tiled kernel (bf16,
+// back-to-back calls):
 // N=1 L=S=128 H=16 E=64 causal 8.5 -> 4.9 us, N=1 L=S=128 H=32 E=128 11.4 -> 6.3 us,
 // N=4 (512 row blocks) 11.9 -> 8.3 us; even at 2048 row blocks (N=16) 26.5 -> 26.0
 // us, and slower at 4096 (N=8 L=512 S=128: 29.4 -> 45.5 us), where the tiled
 // kernel's 256-row passes reuse each key tile for more rows.
-constexpr int64_t kSmallMaxKeys = 128;
+constexpr int64_t kSmallMaxKeys = 256;
 constexpr int kSmallRows = 32;
 constexpr int64_t kSmallMaxBlocks = 1024;
-__host__ __device__ inline int64_t small_max_keys(int E) { return E <= 64 ? 2 * kSmallMaxKeys : kSmallMaxKeys; }
-// Row blocks that run at once: one wave per SIMD (4 per CU) on 256 CUs, except
-// that at E = 64 past 192 keys the staged V rows (42-48 KB of LDS per block) let
-// only 3 blocks share a CU.  A call that needed a second round measured slower
-// than the tiled kernel (N=4 L=S=256 H=32 E=64 causal: 12.3 against 17.6 us).
+// LDS rows of the short-key kernel's staged V: E bf16 padded to small_rsv(E)
+// 16-byte chunks.  The 32 lanes a transposed read serves together read 4 rows x
+// two 32-byte segments; a stride of 4 or 12 chunks mod 16 puts the 4 rows 16
+// banks apart.
+__host__ __device__ constexpr int small_rsv(int E) { return E == 128 ? 20 : (E == 64 ? 12 : 4); }
+// Row blocks that run at once: one wave per SIMD (4 one-wave blocks per CU) on
+// 256 CUs, as far as each block's staged V rows (LDS, 160 KB per CU) allow: E = 64
+// past 192 keys 3 per CU, E = 128 past 128 keys 3 or 2.  A call that needed a
+// second round measured slower than the tiled kernel (N=4 L=S=256 H=32 E=64
+// causal: 12.3 against 17.6 us).
+constexpr int64_t kSmallCuLds = 160 * 1024;
 __host__ __device__ inline int64_t small_max_blocks(int64_t seq_k, int E) {
-  return E == 64 && seq_k > 192 ? 3 * 256 : kSmallMaxBlocks;
+  const int64_t lds = ((seq_k + 31) / 32) * 32 * small_rsv(E) * 16;
+  const int64_t per_cu = kSmallCuLds / lds;
+  const int64_t blocks = 256 * (per_cu < 4 ? per_cu : 4);
+  return blocks < kSmallMaxBlocks ? blocks : kSmallMaxBlocks;
 }
 __host__ __device__ inline bool small_route(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, int E,
                                             bool bf16) {
-  return bf16 && seq_k <= small_max_keys(E) &&
+  return bf16 && seq_k <= kSmallMaxKeys &&
          batch * heads * ((seq_q + kSmallRows - 1) / kSmallRows) <= small_max_blocks(seq_k, E);
 }
 constexpr int kRowsWaves = 8;                 // waves per block

@@ -1,5 +1,4 @@
-// Dense bf16 prefill over short key ranges (at most small_max_keys(E) keys: 256
-// for head dims up to 64, else 128): the
+// Dense bf16 prefill over short key ranges (at most kSmallMaxKeys = 256 keys): the
 // reference's flash_attn_func (flash_attn.mojo:127-183) for calls such as a short
 // prompt, where every key fits in registers.  The tiled kernel would spend such a
 // call on its per-pass pipeline (first-tile waits, the first softmax, the last
@@ -63,10 +62,6 @@ __host__ __device__ inline int small_pv_key(int u, int hf, int t) { return small
 // The key row a load of key `key` reads: keys past the last read the last.
 __host__ __device__ inline int small_clamp_key(int key, int S) { return key < S ? key : S - 1; }
 
-// LDS rows of the staged V: E bf16 padded to kSmallRsv(E) 16-byte chunks.  The
-// 32 lanes a transposed read serves together read 4 rows x two 32-byte segments;
-// a stride of 4 or 12 chunks mod 16 puts the 4 rows 16 banks apart.
-__host__ __device__ constexpr int small_rsv(int E) { return E == 128 ? 20 : (E == 64 ? 12 : 4); }
 
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 small_bf16x4;
 typedef __attribute__((address_space(3))) small_bf16x4 small_lds_bf16x4;
@@ -206,10 +201,10 @@ static int small_launch_t(const FlashParams& p, const FlashPlan& plan, hipStream
     case 2: hipLaunchKernelGGL((flash_small_kernel<E, 2>), grid, block, 0, stream, p); break;
     case 3: hipLaunchKernelGGL((flash_small_kernel<E, 3>), grid, block, 0, stream, p); break;
     case 4: hipLaunchKernelGGL((flash_small_kernel<E, 4>), grid, block, 0, stream, p); break;
-    case 5: if constexpr (E <= 64) { hipLaunchKernelGGL((flash_small_kernel<E, 5>), grid, block, 0, stream, p); break; } return CA_DECLINED;
-    case 6: if constexpr (E <= 64) { hipLaunchKernelGGL((flash_small_kernel<E, 6>), grid, block, 0, stream, p); break; } return CA_DECLINED;
-    case 7: if constexpr (E <= 64) { hipLaunchKernelGGL((flash_small_kernel<E, 7>), grid, block, 0, stream, p); break; } return CA_DECLINED;
-    case 8: if constexpr (E <= 64) { hipLaunchKernelGGL((flash_small_kernel<E, 8>), grid, block, 0, stream, p); break; } return CA_DECLINED;
+    case 5: hipLaunchKernelGGL((flash_small_kernel<E, 5>), grid, block, 0, stream, p); break;
+    case 6: hipLaunchKernelGGL((flash_small_kernel<E, 6>), grid, block, 0, stream, p); break;
+    case 7: hipLaunchKernelGGL((flash_small_kernel<E, 7>), grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((flash_small_kernel<E, 8>), grid, block, 0, stream, p); break;
     default: return CA_DECLINED;
   }
   return ca_launch_status();

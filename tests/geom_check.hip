@@ -270,7 +270,7 @@ static bool check_rows(const FlashParams& p, const FlashPlan& plan, const Ten& q
 template <int E>
 static bool check_small(const FlashParams& p, const FlashPlan& plan, const Ten& q, const Ten& k, const Ten& v) {
   const int L = (int)p.seq_q, S = (int)p.seq_k, NKB = (int)cdiv(S, 32);
-  if (NKB < 1 || 32 * NKB > small_max_keys(E) + 31) FAIL("small: %d key blocks", NKB);
+  if (NKB < 1 || 32 * NKB > kSmallMaxKeys + 31) FAIL("small: %d key blocks", NKB);
   const int64_t nrb = cdiv(L, kSmallRows);
   if (plan.gx != p.batch * p.heads * nrb || plan.gy != 1) FAIL("small: grid");
   std::vector<char> seen((size_t)plan.gx, 0);

@@ -360,9 +360,8 @@ def strided(x, layout):
                                        (1, 64, 1, 8), (2, 31, 64, 5), (1, 96, 32, 1), (1, 256, 256, 4),
                                        (2, 129, 129, 3), (1, 40, 193, 2), (1, 250, 225, 2)])
 def test_short_key_ranges(cuda, d, causal, layout, b, sq, sk, h):
-    """bf16 calls of at most 128 keys, or 256 at head dims up to 64 (the short-key
-    route: one wave per 32 query rows, every key in registers; E = 128 past 128
-    keys takes the tiled kernel): partial 32-key blocks, a single key, more rows
+    """bf16 calls of at most 256 keys (the short-key route: one wave per 32 query
+    rows, every key in registers): partial 32-key blocks, a single key, more rows
     than keys (causal rows that see no key are 0), more keys than rows, partial
     32-row blocks, and q/k/v read in place from fused or head-major views."""
     g = torch.Generator().manual_seed(sq * 131 + sk)
@@ -374,15 +373,17 @@ def test_short_key_ranges(cuda, d, causal, layout, b, sq, sk, h):
         assert torch.count_nonzero(out[:, :sq - sk]) == 0
 
 
-@pytest.mark.parametrize("b,sq,sk,h,d", [(8, 128, 128, 32, 64), (8, 129, 128, 32, 64), (2, 32, 129, 4, 128),
-                                         (2, 32, 256, 4, 64), (2, 32, 257, 4, 64), (3, 256, 256, 32, 64),
-                                         (4, 256, 256, 32, 64), (4, 256, 192, 32, 64), (8, 256, 256, 16, 32)])
+@pytest.mark.parametrize("b,sq,sk,h,d", [(8, 128, 128, 32, 64), (8, 129, 128, 32, 64), (2, 32, 256, 4, 64),
+                                         (2, 32, 257, 4, 64), (3, 256, 256, 32, 64), (4, 256, 256, 32, 64),
+                                         (4, 256, 192, 32, 64), (8, 256, 256, 16, 32), (2, 256, 256, 32, 128),
+                                         (3, 256, 256, 32, 128), (3, 160, 160, 32, 128), (4, 160, 160, 32, 128)])
 def test_short_key_route_edges(cuda, b, sq, sk, h, d):
     """Either side of the short-key route's limits: 8 x 32 x 4 = 1024 row blocks
-    (taken), 8 x 32 x 5 = 1280 (the tiled kernel); at E = 128 129 keys (tiled); at
-    E = 64 256 keys (taken) and 257 (tiled), and past 192 keys 768 row blocks
-    (taken) against 1024 (tiled; 192 keys: taken); at E = 32 1024 blocks of 256
-    keys (taken).  Checked on the first and last heads."""
+    (taken), 8 x 32 x 5 = 1280 (the tiled kernel); 256 keys (taken) against 257
+    (tiled); the row blocks whose staged V rows fit the CUs at once: E = 64 past
+    192 keys 768 (taken) against 1024 (tiled; 192 keys: taken), E = 128 at 256 keys
+    512 against 768, at 160 keys 768 against 1024; E = 32 1024 blocks of 256 keys
+    (taken).  Checked on the first and last heads."""
     g = torch.Generator().manual_seed(sq + sk)
     q, k, v = (torch.randn(b, n, h, d, generator=g).bfloat16().to(cuda) for n in (sq, sk, sk))
     out = flash_attn_func(q, k, v, causal=True)

@@ -71,9 +71,9 @@ def shapes():
             for causal in (False, True):
                 for lay in ("bshe", "fused", "bhse"):
                     out.append(line(e, True, causal, b, sq, sk, h, lay))
-    # the short-key route past 128 keys (head dims up to 64; E = 128 goes tiled)
+    # the short-key route past 128 keys, and the row-block limits its LDS sets
     for b, sq, sk, h in [(1, 256, 256, 16), (8, 256, 256, 16), (2, 129, 129, 3), (1, 200, 255, 4), (3, 37, 193, 2),
-                         (4, 512, 256, 8)]:
+                         (4, 512, 256, 8), (2, 256, 256, 32), (3, 256, 256, 32), (3, 160, 160, 32)]:
         for e in (32, 64, 128):
             for causal in (False, True):
                 for lay in ("bshe", "fused", "bhse"):
