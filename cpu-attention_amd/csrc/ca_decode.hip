@@ -412,6 +412,9 @@ __device__ __forceinline__ int merge_count_in(uint64_t* ctr, uint32_t tag) {
 
 // One wave per TK-key tile of each row, 8 tiles per block merged in LDS.
 // APPEND: the call's one-token append is done here (p.k_new).
+template <int E, bool BF, bool COHERENT>
+__device__ __forceinline__ void merge_partials(const DecodeParams& p, int64_t row, int n, int lane);
+
 template <int E, bool BF, bool APPEND, int TK>
 __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(4)))
 void decode_tiles_kernel(DecodeParams p) {

@@ -1187,7 +1187,7 @@ __global__ __launch_bounds__(256, 2) void flash_f32_kernel(FlashParams p) {
   const int64_t row = bw.q0 + 32 * wv + li;
   const int sp = SPLIT ? (int)blockIdx.y : 0, splits = SPLIT ? (int)gridDim.y : 1;
   const F32Keys kr_ = f32_keys(p, bw.q0, SPLIT, sp, splits);
-  const int64_t kbeg = kr_.kbeg, kend_blk = kr_.kend;
+  const int64_t kbeg = kr_.kbeg;
   // The partial slot of (row, split): O at part_acc[slot * E], (max, sum) at part_ml[2 * slot].
   const int64_t slot = ((bw.b * p.heads + bw.h) * L + row) * splits + sp;
   const int nkt = kr_.nkt;
