@@ -138,8 +138,13 @@ constexpr int64_t kRowsMaxSplits = 64;
 // blocks) 4 splits 109.1 us, 3 splits 136.6 us; L=100 S=4096 H=300 (300) 2 splits
 // 428.2 us, unsplit 570.7 us; but L=640 S=2048 H=24 (120) 5 splits 187.2 us, 4
 // splits 152.0 us.  bf16 calls with fewer than twice as many keys as rows do not split: if
-// causal, because the causal triangle is most of their work and the unsplit
-// blocks finish sooner (N=1 L=1024 H=32 E=128: 41.1 -> 33.8 us); if not, once they
+// causal, once they have kTiledMinItemsUnsplit query blocks or fewer than
+// kTiledMinKeysCausal keys, because the causal triangle is most of their work and
+// the unsplit blocks finish sooner (N=1 L=1024 H=32 E=128: 41.1 -> 33.8 us; N=1
+// L=S=512 H=16 E=64, 32 query blocks: 18.6 -> 16.6 us), while longer ones with few
+// query blocks leave most CUs idle unsplit (N=1 L=S=2048 H=4 E=128: 30.3 against
+// 53.8 us, L=S=1024 H=8 E=128 27.5 against 32.3 us, L=S=1500 H=10 E=64 25.9
+// against 32.5 us); if not, once they
 // have kTiledMinItemsUnsplit query blocks, because the partials (fp32 (E + 2) per
 // row and split, written and read back) cost more than the shorter walks save
 // (N=1 L=S=1024 H=32 E=128: 39.7 -> 31.3 us, L=S=1500 H=20 E=64: 34.6 -> 31.5 us),
@@ -151,12 +156,14 @@ constexpr int64_t kTiledTargetBlocks = 256;
 constexpr int64_t kTiledMinKeys = 256;
 constexpr int64_t kTiledMaxSplits = 64;
 constexpr int64_t kTiledMinItemsUnsplit = 64;
+constexpr int64_t kTiledMinKeysCausal = 1024;
 __host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads,
                                                 bool bf16, bool causal) {
   if (rows_route(batch, seq_q, heads, bf16)) return 1;
-  if (bf16 && causal && seq_k < 2 * seq_q) return 1;
   const int64_t bm = bf16 ? 256 : 128;
   const int64_t items = batch * heads * ((seq_q + bm - 1) / bm);
+  if (bf16 && causal && seq_k < 2 * seq_q && (items >= kTiledMinItemsUnsplit || seq_k < kTiledMinKeysCausal))
+    return 1;
   if (bf16 && seq_k < 2 * seq_q && items >= kTiledMinItemsUnsplit) return 1;
   const int64_t target = bf16 ? kTiledTargetBlocks : 2 * kTiledTargetBlocks;
   if (items <= 0 || items >= target) return 1;

@@ -233,7 +233,8 @@ def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq, h):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("b,sq,sk,h", [(1, 600, 600, 130), (1, 400, 400, 8), (1, 2048, 2048, 32),
-                                       (2, 700, 1200, 48), (1, 2048, 4096, 32), (1, 1024, 1024, 16)])
+                                       (2, 700, 1200, 48), (1, 2048, 4096, 32), (1, 1024, 1024, 16),
+                                       (1, 2048, 2048, 4), (1, 1500, 1500, 10), (1, 512, 512, 16)])
 def test_causal_block_schedules(cuda, d, b, sq, sk, h, dtype):
     """The causal block schedules, each checked on a few heads: query-block pairs
     (qb, nqb-1-qb) in one block when unpaired blocks would leave the chip
@@ -244,7 +245,9 @@ def test_causal_block_schedules(cuda, d, b, sq, sk, h, dtype):
     from 1024, or from 512 with fewer than twice as many keys as rows: 650, 576
     and 512 at L = S = 2048 pair (odd and even counts per head); 32, and 512 over
     4096 keys, do not.  64 bf16 query blocks at L = S = 1024 run unsplit (causal
-    triangle); the same call in fp32 (128 query blocks) splits its keys."""
+    triangle); the same call in fp32 (128 query blocks) splits its keys.  Fewer
+    bf16 query blocks over at least 1024 keys split (32 at L = S = 2048: 8 splits;
+    60 at L = S = 1500: 4), over 512 keys they do not."""
     g = torch.Generator().manual_seed(40 + h)
     q = torch.randn(b, sq, h, d, generator=g).to(dtype).to(cuda)
     k, v = (torch.randn(b, sk, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))
@@ -294,7 +297,8 @@ def test_split_keys(cuda, d, causal, shape, dtype):
 def test_split_keys_rows_without_keys(cuda, dtype):
     """Causal with more query rows than keys: the first rows see no key (exactly
     0).  fp32 splits the keys over blocks (every split of those rows is empty);
-    bf16 causal calls with fewer than twice as many keys as rows do not split."""
+    bf16 causal calls with fewer than twice as many keys as rows do not split
+    below 1024 keys."""
     g = torch.Generator().manual_seed(32)
     q = torch.randn(1, 700, 4, 64, generator=g).to(dtype).to(cuda)
     k, v = (torch.randn(1, 600, 4, 64, generator=g).to(dtype).to(cuda) for _ in range(2))
