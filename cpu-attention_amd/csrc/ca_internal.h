@@ -138,20 +138,23 @@ constexpr int64_t kRowsMaxSplits = 64;
 // blocks) 4 splits 109.1 us, 3 splits 136.6 us; L=100 S=4096 H=300 (300) 2 splits
 // 428.2 us, unsplit 570.7 us; but L=640 S=2048 H=24 (120) 5 splits 187.2 us, 4
 // splits 152.0 us.  bf16 calls with fewer than twice as many keys as rows do not split: if
-// causal, once they have kTiledMinItemsUnsplit query blocks or fewer than
-// kTiledMinKeysCausal keys, because the causal triangle is most of their work and
-// the unsplit blocks finish sooner (N=1 L=1024 H=32 E=128: 41.1 -> 33.8 us; N=1
-// L=S=512 H=16 E=64, 32 query blocks: 18.6 -> 16.6 us), while longer ones with few
-// query blocks leave most CUs idle unsplit (N=1 L=S=2048 H=4 E=128: 30.3 against
-// 53.8 us, L=S=1024 H=8 E=128 27.5 against 32.3 us, L=S=1500 H=10 E=64 25.9
-// against 32.5 us); if not, once they
+// causal, below kTiledMinKeysCausal keys, from 2 * kTiledMinItemsUnsplit query
+// blocks, and from kTiledMinItemsUnsplit below 2 * kTiledMinKeysCausal keys, because
+// the causal triangle is most of their work and the unsplit blocks finish sooner
+// (N=1 L=1024 H=32 E=128: 41.1 -> 33.8 us; N=1 L=S=512 H=16 E=64, 32 query
+// blocks: 18.6 -> 16.6 us; L=S=1500 H=20 E=64, 120: 32.7 -> 34.6 us split), while
+// longer ones with fewer query blocks leave most CUs idle unsplit (N=1 L=S=2048
+// H=4 E=128: 30.3 against 53.8 us; L=S=1500 H=10 E=64 25.9 against 32.5 us; 64 to
+// 127 query blocks over 2048 keys or more: N=1 L=S=4096 H=4 E=128 47.0 against
+// 97.2 us, L=S=2048 H=8 E=64 27.9 against 40.8 us, L=S=2048 H=12 E=128 49.3
+// against 54.1 us); if not, once they
 // have kTiledMinItemsUnsplit query blocks, because the partials (fp32 (E + 2) per
 // row and split, written and read back) cost more than the shorter walks save
 // (N=1 L=S=1024 H=32 E=128: 39.7 -> 31.3 us, L=S=1500 H=20 E=64: 34.6 -> 31.5 us),
 // while fewer query blocks leave most CUs idle (N=2 L=700 S=1200 H=8 E=64, 48
 // blocks: split 23.0 us, unsplit 26.1 us).  fp32 calls split (193 -> 301 us
-// unsplit at L=1280 causal).  So a causal call never splits more than the
-// non-causal call of the same shapes, which the workspace query answers for.
+// unsplit at L=1280 causal).  A causal call can so split more than the
+// non-causal call of the same shapes: the workspace query answers for the larger.
 constexpr int64_t kTiledTargetBlocks = 256;
 constexpr int64_t kTiledMinKeys = 256;
 constexpr int64_t kTiledMaxSplits = 64;
@@ -162,9 +165,12 @@ __host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, in
   if (rows_route(batch, seq_q, heads, bf16)) return 1;
   const int64_t bm = bf16 ? 256 : 128;
   const int64_t items = batch * heads * ((seq_q + bm - 1) / bm);
-  if (bf16 && causal && seq_k < 2 * seq_q && (items >= kTiledMinItemsUnsplit || seq_k < kTiledMinKeysCausal))
-    return 1;
-  if (bf16 && seq_k < 2 * seq_q && items >= kTiledMinItemsUnsplit) return 1;
+  if (bf16 && seq_k < 2 * seq_q) {
+    if (!causal && items >= kTiledMinItemsUnsplit) return 1;
+    if (causal && (seq_k < kTiledMinKeysCausal || items >= 2 * kTiledMinItemsUnsplit ||
+                   (items >= kTiledMinItemsUnsplit && seq_k < 2 * kTiledMinKeysCausal)))
+      return 1;
+  }
   const int64_t target = bf16 ? kTiledTargetBlocks : 2 * kTiledTargetBlocks;
   if (items <= 0 || items >= target) return 1;
   int64_t s = bf16 ? target / items : (target + items - 1) / items;
@@ -178,6 +184,13 @@ __host__ __device__ inline int64_t tiled_workspace_bytes(int64_t batch, int64_t 
                                                          int64_t heads, int E, bool bf16, bool causal) {
   const int64_t s = tiled_splits(batch, seq_q, seq_k, heads, bf16, causal);
   return s > 1 ? batch * heads * seq_q * s * (E + 2) * 4 : 0;
+}
+// The same for a call whose causal flag the caller does not state: the larger.
+__host__ __device__ inline int64_t tiled_workspace_bytes_any(int64_t batch, int64_t seq_q, int64_t seq_k,
+                                                             int64_t heads, int E, bool bf16) {
+  const int64_t a = tiled_workspace_bytes(batch, seq_q, seq_k, heads, E, bf16, false);
+  const int64_t c = tiled_workspace_bytes(batch, seq_q, seq_k, heads, E, bf16, true);
+  return a > c ? a : c;
 }
 
 // The decode kernel does a one-token append itself (rather than a store kernel

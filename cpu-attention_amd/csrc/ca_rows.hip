@@ -616,10 +616,10 @@ __host__ __device__ inline int64_t rows_ws_bytes(int64_t rows, int64_t splits, i
 
 // The workspace a call of these shapes may need: its strides are not known
 // here, so the larger of the two routes' partials; past the few-rows route, the
-// tiled kernel's split mode.
+// tiled kernel's split mode, causal or not.
 int64_t flash_rows_workspace_bytes(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads, int E,
                                    bool bf16) {
-  if (!rows_route(batch, seq_q, heads, bf16)) return tiled_workspace_bytes(batch, seq_q, seq_k, heads, E, bf16, false);
+  if (!rows_route(batch, seq_q, heads, bf16)) return tiled_workspace_bytes_any(batch, seq_q, seq_k, heads, E, bf16);
   int64_t splits = rows_splits(batch, seq_q, seq_k, heads, E, bf16);
   if (rows_heads_shapes(seq_q, heads, E, bf16)) {
     const int64_t hs = rows_heads_splits(batch, seq_k, heads, E, bf16);

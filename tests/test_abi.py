@@ -174,29 +174,41 @@ def test_flash_workspace_for_few_rows(dtype, d, chunk):
 
 
 def tiled(b, sq, sk, h, d, dtype):
-    """The tiled prefill's split mode (non-causal, which the workspace query
-    answers for): when its query blocks (b * h * ceil(sq / rows per block): 256 in
-    bf16, 128 in fp32) number fewer than a target (256 in bf16, 512 in fp32), each
-    one's keys are split over target / blocks blocks (rounded down in bf16: one
-    round of the chip; up in fp32), at least 256 keys each (whole
-    64-key units) and at most 64 splits,
-    which needs (E + 2) floats per (batch, head, row, split); except bf16 calls
-    with fewer than twice as many keys as rows and at least 64 query blocks, and
-    short key ranges (128 keys or fewer) in bf16, which do not split."""
+    """The tiled prefill's split mode: when its query blocks (b * h * ceil(sq /
+    rows per block): 256 in bf16, 128 in fp32) number fewer than a target (256 in
+    bf16, 512 in fp32), each one's keys are split over target / blocks blocks
+    (rounded down in bf16: one round of the chip; up in fp32), at least 256 keys
+    each (whole 64-key units) and at most 64 splits, which needs (E + 2) floats
+    per (batch, head, row, split).  bf16 calls with fewer than twice as many keys
+    as rows and at least 64 query blocks do not split, unless causal with fewer
+    than 128 query blocks over 2048 keys or more; causal ones under 1024 keys do
+    not split at all.  The query answers for the larger of the causal and
+    non-causal call."""
     blocks = b * h * -(-sq // (256 if dtype == 1 else 128))
     target = 256 if dtype == 1 else 512
-    if blocks >= target or (dtype == 1 and sk < 2 * sq and blocks >= 64):
-        return 0
-    per = target // blocks if dtype == 1 else -(-target // blocks)
-    splits = min(per, -(-sk // 64) // 4, 64)
-    return 0 if splits < 2 else b * h * sq * splits * (d + 2) * 4
+
+    def splits(causal):
+        if blocks >= target:
+            return 1
+        if dtype == 1 and sk < 2 * sq:
+            if not causal and blocks >= 64:
+                return 1
+            if causal and (sk < 1024 or blocks >= 128 or (blocks >= 64 and sk < 2048)):
+                return 1
+        per = target // blocks if dtype == 1 else -(-target // blocks)
+        return min(per, -(-sk // 64) // 4, 64)
+
+    s = max(splits(False), splits(True))
+    return 0 if s < 2 else b * h * sq * s * (d + 2) * 4
 
 
 @pytest.mark.parametrize("d", [32, 64, 128])
 def test_flash_workspace_for_split_keys(d):
     lib = K.load_library()
     for b, sq, sk, h in ((1, 64, 4096, 32), (1, 17, 2100, 8), (2, 300, 1500, 4), (4, 4096, 4096, 32),
-                         (1, 128, 128, 16), (1, 600, 255, 3), (1, 5, 100000, 1), (1, 100, 4096, 300)):
+                         (1, 128, 128, 16), (1, 600, 255, 3), (1, 5, 100000, 1), (1, 100, 4096, 300),
+                         (1, 4096, 4096, 4), (1, 2048, 2048, 12), (1, 1024, 1024, 8), (1, 512, 512, 16),
+                         (1, 1500, 1500, 20)):
         assert lib.ca_flash_workspace_bytes(b, sq, sk, h, d, 1) == tiled(b, sq, sk, h, d, 1)
         if sq > 16:  # fp32 past the few-rows route
             assert lib.ca_flash_workspace_bytes(b, sq, sk, h, d, 0) == tiled(b, sq, sk, h, d, 0)
@@ -215,6 +227,10 @@ def test_flash_workspace_for_split_keys(d):
     # bf16, keys under twice the rows: 64 query blocks or more do not split, fewer do
     assert lib.ca_flash_workspace_bytes(1, 1024, 1024, 16, d, 1) == 0
     assert lib.ca_flash_workspace_bytes(2, 700, 1200, 8, d, 1) == 2 * 8 * 700 * 4 * (d + 2) * 4
+    # ... except causal calls of 64 to 127 query blocks over 2048 keys or more, whose
+    # splits the query answers for: L=S=4096 H=4 (64 query blocks) 4 splits
+    assert lib.ca_flash_workspace_bytes(1, 4096, 4096, 4, d, 1) == 4 * 4096 * 4 * (d + 2) * 4
+    assert lib.ca_flash_workspace_bytes(1, 1500, 1500, 20, d, 1) == 0  # 120 query blocks under 2048 keys
 
 
 def test_missing_library_is_a_loud_error(monkeypatch):
