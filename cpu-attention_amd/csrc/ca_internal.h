@@ -137,40 +137,35 @@ constexpr int64_t kRowsMaxSplits = 64;
 // up, and neither rounding wins everywhere: causal L=S=1280 H=16 (160 query
 // blocks) 4 splits 109.1 us, 3 splits 136.6 us; L=100 S=4096 H=300 (300) 2 splits
 // 428.2 us, unsplit 570.7 us; but L=640 S=2048 H=24 (120) 5 splits 187.2 us, 4
-// splits 152.0 us.  bf16 calls with fewer than twice as many keys as rows do not split: if
-// causal, below kTiledMinKeysCausal keys, from 2 * kTiledMinItemsUnsplit query
-// blocks, and from kTiledMinItemsUnsplit below 2 * kTiledMinKeysCausal keys, because
-// the causal triangle is most of their work and the unsplit blocks finish sooner
-// (N=1 L=1024 H=32 E=128: 41.1 -> 33.8 us; N=1 L=S=512 H=16 E=64, 32 query
-// blocks: 18.6 -> 16.6 us; L=S=1500 H=20 E=64, 120: 32.7 -> 34.6 us split), while
-// longer ones with fewer query blocks leave most CUs idle unsplit (N=1 L=S=2048
-// H=4 E=128: 30.3 against 53.8 us; L=S=1500 H=10 E=64 25.9 against 32.5 us; 64 to
-// 127 query blocks over 2048 keys or more: N=1 L=S=4096 H=4 E=128 47.0 against
-// 97.2 us, L=S=2048 H=8 E=64 27.9 against 40.8 us, L=S=2048 H=12 E=128 49.3
-// against 54.1 us); if not, once they
-// have kTiledMinItemsUnsplit query blocks, because the partials (fp32 (E + 2) per
-// row and split, written and read back) cost more than the shorter walks save
-// (N=1 L=S=1024 H=32 E=128: 39.7 -> 31.3 us, L=S=1500 H=20 E=64: 34.6 -> 31.5 us),
-// while fewer query blocks leave most CUs idle (N=2 L=700 S=1200 H=8 E=64, 48
-// blocks: split 23.0 us, unsplit 26.1 us).  fp32 calls split (193 -> 301 us
-// unsplit at L=1280 causal).  A causal call can so split more than the
-// non-causal call of the same shapes: the workspace query answers for the larger.
+// splits 152.0 us.  bf16 calls with fewer than twice as many keys as rows do not split
+// from 2 * kTiledMinItemsUnsplit query blocks, nor from kTiledMinItemsUnsplit under
+// kTiledMinKeysLong keys, nor, if causal, under kTiledMinKeysCausal keys: the
+// partials (fp32 (E + 2) per row and split, written and read back) and, for causal
+// calls, a triangle that is most of the work make the unsplit blocks finish sooner
+// (N=1 L=S=1024 H=32 E=128 non-causal 39.7 -> 31.3 us, causal 41.1 -> 33.8 us;
+// L=S=1500 H=20 E=64: 34.6 -> 31.5 us; causal L=S=512 H=16 E=64, 32 query blocks,
+// 18.6 -> 16.6 us).  With fewer query blocks, or 64 to 127 over longer keys, most
+// CUs would sit idle unsplit (N=2 L=700 S=1200 H=8 E=64, 48 blocks: split 23.0 us,
+// unsplit 26.1 us; N=1 L=S=4096 H=4 E=128, 64: non-causal 51.6 against 96.1 us,
+// causal 47.0 against 97.2 us; L=S=2048 H=8 E=64 26.3 / 27.9 against 38.6 / 40.8
+// us; causal L=S=2048 H=4 E=128, 32: 30.3 against 53.8 us).  fp32 calls split (193
+// -> 301 us unsplit at L=1280 causal).  A causal call never splits more than the
+// non-causal call of the same shapes; the workspace query answers for both.
 constexpr int64_t kTiledTargetBlocks = 256;
 constexpr int64_t kTiledMinKeys = 256;
 constexpr int64_t kTiledMaxSplits = 64;
 constexpr int64_t kTiledMinItemsUnsplit = 64;
 constexpr int64_t kTiledMinKeysCausal = 1024;
+constexpr int64_t kTiledMinKeysLong = 2048;
 __host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads,
                                                 bool bf16, bool causal) {
   if (rows_route(batch, seq_q, heads, bf16)) return 1;
   const int64_t bm = bf16 ? 256 : 128;
   const int64_t items = batch * heads * ((seq_q + bm - 1) / bm);
-  if (bf16 && seq_k < 2 * seq_q) {
-    if (!causal && items >= kTiledMinItemsUnsplit) return 1;
-    if (causal && (seq_k < kTiledMinKeysCausal || items >= 2 * kTiledMinItemsUnsplit ||
-                   (items >= kTiledMinItemsUnsplit && seq_k < 2 * kTiledMinKeysCausal)))
-      return 1;
-  }
+  if (bf16 && seq_k < 2 * seq_q &&
+      (items >= 2 * kTiledMinItemsUnsplit || (items >= kTiledMinItemsUnsplit && seq_k < kTiledMinKeysLong) ||
+       (causal && seq_k < kTiledMinKeysCausal)))
+    return 1;
   const int64_t target = bf16 ? kTiledTargetBlocks : 2 * kTiledTargetBlocks;
   if (items <= 0 || items >= target) return 1;
   int64_t s = bf16 ? target / items : (target + items - 1) / items;

@@ -182,8 +182,9 @@ int ca_decode_noalloc(const ca_decode_args* args, void* stream);
  * workspace: few-row calls (seq_q <= 4 bf16; <= 8 fp32, or <= 16 with batch x
  * heads >= 256), and calls with fewer
  * than 256 query blocks of 256 rows (bf16) or 512 of 128 rows (fp32) over long
- * key ranges (bf16 causal calls with fewer than twice as many keys as rows only
- * below 64 query blocks over 1024 keys or more, or below 128 over 2048 or more).
+ * key ranges (bf16 calls with fewer than twice as many keys as rows only below
+ * 64 query blocks, or below 128 over 2048 keys or more; causal ones only over
+ * 1024 keys or more).
  * Pass at least the bytes ca_flash_workspace_bytes() asks for (0 means none is
  * needed; it answers for the larger of the causal and non-causal call; a
  * shorter workspace declines the call), 16-byte aligned (256 recommended; a

@@ -180,21 +180,18 @@ def tiled(b, sq, sk, h, d, dtype):
     (rounded down in bf16: one round of the chip; up in fp32), at least 256 keys
     each (whole 64-key units) and at most 64 splits, which needs (E + 2) floats
     per (batch, head, row, split).  bf16 calls with fewer than twice as many keys
-    as rows and at least 64 query blocks do not split, unless causal with fewer
-    than 128 query blocks over 2048 keys or more; causal ones under 1024 keys do
-    not split at all.  The query answers for the larger of the causal and
-    non-causal call."""
+    as rows do not split from 128 query blocks, nor from 64 under 2048 keys, nor,
+    if causal, under 1024 keys.  The query answers for the larger of the causal
+    and non-causal call."""
     blocks = b * h * -(-sq // (256 if dtype == 1 else 128))
     target = 256 if dtype == 1 else 512
 
     def splits(causal):
         if blocks >= target:
             return 1
-        if dtype == 1 and sk < 2 * sq:
-            if not causal and blocks >= 64:
-                return 1
-            if causal and (sk < 1024 or blocks >= 128 or (blocks >= 64 and sk < 2048)):
-                return 1
+        if dtype == 1 and sk < 2 * sq and (blocks >= 128 or (blocks >= 64 and sk < 2048) or
+                                           (causal and sk < 1024)):
+            return 1
         per = target // blocks if dtype == 1 else -(-target // blocks)
         return min(per, -(-sk // 64) // 4, 64)
 
@@ -227,8 +224,8 @@ def test_flash_workspace_for_split_keys(d):
     # bf16, keys under twice the rows: 64 query blocks or more do not split, fewer do
     assert lib.ca_flash_workspace_bytes(1, 1024, 1024, 16, d, 1) == 0
     assert lib.ca_flash_workspace_bytes(2, 700, 1200, 8, d, 1) == 2 * 8 * 700 * 4 * (d + 2) * 4
-    # ... except causal calls of 64 to 127 query blocks over 2048 keys or more, whose
-    # splits the query answers for: L=S=4096 H=4 (64 query blocks) 4 splits
+    # ... except 64 to 127 query blocks over 2048 keys or more: L=S=4096 H=4 (64
+    # query blocks) 4 splits
     assert lib.ca_flash_workspace_bytes(1, 4096, 4096, 4, d, 1) == 4 * 4096 * 4 * (d + 2) * 4
     assert lib.ca_flash_workspace_bytes(1, 1500, 1500, 20, d, 1) == 0  # 120 query blocks under 2048 keys
 

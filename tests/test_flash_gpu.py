@@ -249,7 +249,8 @@ def test_causal_block_schedules(cuda, d, b, sq, sk, h, dtype):
     triangle); the same call in fp32 (128 query blocks) splits its keys.  Fewer
     bf16 query blocks over at least 1024 keys split (32 at L = S = 2048: 8 splits;
     60 at L = S = 1500: 4), over 512 keys they do not; 64 to 127 split over 2048
-    keys or more (64 at L = S = 4096: 4 splits), not below (120 at L = S = 1500)."""
+    keys or more (64 at L = S = 4096: 4 splits), not below (120 at L = S = 1500),
+    causal or not."""
     g = torch.Generator().manual_seed(40 + h)
     q = torch.randn(b, sq, h, d, generator=g).to(dtype).to(cuda)
     k, v = (torch.randn(b, sk, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))

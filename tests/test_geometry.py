@@ -83,10 +83,12 @@ def shapes():
     big = 12 << 20
     out.append(" ".join(str(x) for x in (64, 1, 1, 1, 200, 200, 2, 200 * big, big, 64, 200 * big, big, 64,
                                           200 * big, big, 64)))
-    # causal calls with keys under twice the rows that split (few query blocks)
+    # calls with keys under twice the rows that split (few query blocks)
     for e in (64, 128):
-        for b, sq, sk, h in [(1, 4096, 4096, 4), (1, 2048, 2048, 12), (1, 1024, 1024, 8), (1, 3000, 3000, 8)]:
-            out.append(line(e, True, True, b, sq, sk, h, "fused"))
+        for b, sq, sk, h in [(1, 4096, 4096, 4), (1, 2048, 2048, 12), (1, 1024, 1024, 8), (1, 3000, 3000, 8),
+                             (1, 1500, 2100, 16)]:
+            for causal in (False, True):
+                out.append(line(e, True, causal, b, sq, sk, h, "fused"))
     # single-row calls on the packed-heads route (split keys, merge counters)
     for b, sq, sk, h in [(8, 1, 2048, 32), (8, 1, 8192, 32), (2, 1, 16384, 16), (32, 1, 2048, 32), (64, 1, 512, 32),
                          (1, 1, 100000, 16), (3, 1, 77, 8)]:
