@@ -138,8 +138,10 @@ constexpr int64_t kRowsMaxSplits = 64;
 // blocks) 4 splits 109.1 us, 3 splits 136.6 us; L=100 S=4096 H=300 (300) 2 splits
 // 428.2 us, unsplit 570.7 us; but L=640 S=2048 H=24 (120) 5 splits 187.2 us, 4
 // splits 152.0 us.  bf16 calls with fewer than twice as many keys as rows do not split
-// from 2 * kTiledMinItemsUnsplit query blocks, nor from kTiledMinItemsUnsplit under
-// kTiledMinKeysLong keys, nor, if causal, under kTiledMinKeysCausal keys: the
+// from 2 * kTiledMinItemsUnsplit query blocks under 2 * kTiledMinKeysLong keys (more
+// query blocks than that round down to one split anyway), nor from
+// kTiledMinItemsUnsplit under kTiledMinKeysLong keys, nor, if causal, under
+// kTiledMinKeysCausal keys: the
 // partials (fp32 (E + 2) per row and split, written and read back) and, for causal
 // calls, a triangle that is most of the work make the unsplit blocks finish sooner
 // (N=1 L=S=1024 H=32 E=128 non-causal 39.7 -> 31.3 us, causal 41.1 -> 33.8 us;
@@ -148,7 +150,9 @@ constexpr int64_t kRowsMaxSplits = 64;
 // CUs would sit idle unsplit (N=2 L=700 S=1200 H=8 E=64, 48 blocks: split 23.0 us,
 // unsplit 26.1 us; N=1 L=S=4096 H=4 E=128, 64: non-causal 51.6 against 96.1 us,
 // causal 47.0 against 97.2 us; L=S=2048 H=8 E=64 26.3 / 27.9 against 38.6 / 40.8
-// us; causal L=S=2048 H=4 E=128, 32: 30.3 against 53.8 us).  fp32 calls split (193
+// us; causal L=S=2048 H=4 E=128, 32: 30.3 against 53.8 us; 128 query blocks over
+// 4096 keys or more, 2 splits: L=S=4096 H=8 E=128 80.8 against 96.3 us, causal 74.2
+// against 97.1 us, causal L=S=8192 H=4 115.8 against 184.5 us).  fp32 calls split (193
 // -> 301 us unsplit at L=1280 causal).  A causal call never splits more than the
 // non-causal call of the same shapes; the workspace query answers for both.
 constexpr int64_t kTiledTargetBlocks = 256;
@@ -163,7 +167,8 @@ __host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, in
   const int64_t bm = bf16 ? 256 : 128;
   const int64_t items = batch * heads * ((seq_q + bm - 1) / bm);
   if (bf16 && seq_k < 2 * seq_q &&
-      (items >= 2 * kTiledMinItemsUnsplit || (items >= kTiledMinItemsUnsplit && seq_k < kTiledMinKeysLong) ||
+      ((items >= 2 * kTiledMinItemsUnsplit && seq_k < 2 * kTiledMinKeysLong) ||
+       (items >= kTiledMinItemsUnsplit && seq_k < kTiledMinKeysLong) ||
        (causal && seq_k < kTiledMinKeysCausal)))
     return 1;
   const int64_t target = bf16 ? kTiledTargetBlocks : 2 * kTiledTargetBlocks;

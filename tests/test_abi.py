@@ -180,16 +180,16 @@ def tiled(b, sq, sk, h, d, dtype):
     (rounded down in bf16: one round of the chip; up in fp32), at least 256 keys
     each (whole 64-key units) and at most 64 splits, which needs (E + 2) floats
     per (batch, head, row, split).  bf16 calls with fewer than twice as many keys
-    as rows do not split from 128 query blocks, nor from 64 under 2048 keys, nor,
-    if causal, under 1024 keys.  The query answers for the larger of the causal
-    and non-causal call."""
+    as rows do not split from 128 query blocks under 4096 keys, nor from 64 under
+    2048 keys, nor, if causal, under 1024 keys.  The query answers for the larger
+    of the causal and non-causal call."""
     blocks = b * h * -(-sq // (256 if dtype == 1 else 128))
     target = 256 if dtype == 1 else 512
 
     def splits(causal):
         if blocks >= target:
             return 1
-        if dtype == 1 and sk < 2 * sq and (blocks >= 128 or (blocks >= 64 and sk < 2048) or
+        if dtype == 1 and sk < 2 * sq and ((blocks >= 128 and sk < 4096) or (blocks >= 64 and sk < 2048) or
                                            (causal and sk < 1024)):
             return 1
         per = target // blocks if dtype == 1 else -(-target // blocks)
@@ -205,7 +205,7 @@ def test_flash_workspace_for_split_keys(d):
     for b, sq, sk, h in ((1, 64, 4096, 32), (1, 17, 2100, 8), (2, 300, 1500, 4), (4, 4096, 4096, 32),
                          (1, 128, 128, 16), (1, 600, 255, 3), (1, 5, 100000, 1), (1, 100, 4096, 300),
                          (1, 4096, 4096, 4), (1, 2048, 2048, 12), (1, 1024, 1024, 8), (1, 512, 512, 16),
-                         (1, 1500, 1500, 20)):
+                         (1, 1500, 1500, 20), (1, 4096, 4096, 8), (1, 4096, 4096, 12), (1, 3000, 3000, 16)):
         assert lib.ca_flash_workspace_bytes(b, sq, sk, h, d, 1) == tiled(b, sq, sk, h, d, 1)
         if sq > 16:  # fp32 past the few-rows route
             assert lib.ca_flash_workspace_bytes(b, sq, sk, h, d, 0) == tiled(b, sq, sk, h, d, 0)
@@ -228,6 +228,9 @@ def test_flash_workspace_for_split_keys(d):
     # query blocks) 4 splits
     assert lib.ca_flash_workspace_bytes(1, 4096, 4096, 4, d, 1) == 4 * 4096 * 4 * (d + 2) * 4
     assert lib.ca_flash_workspace_bytes(1, 1500, 1500, 20, d, 1) == 0  # 120 query blocks under 2048 keys
+    # 128 query blocks over 4096 keys: 2 splits (more than 128 round down to 1)
+    assert lib.ca_flash_workspace_bytes(1, 4096, 4096, 8, d, 1) == 8 * 4096 * 2 * (d + 2) * 4
+    assert lib.ca_flash_workspace_bytes(1, 4096, 4096, 12, d, 1) == 0
 
 
 def test_missing_library_is_a_loud_error(monkeypatch):

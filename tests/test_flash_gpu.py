@@ -235,7 +235,7 @@ def test_every_wave_of_a_block_failing_the_walk(cuda, d, causal, sq, h):
 @pytest.mark.parametrize("b,sq,sk,h", [(1, 600, 600, 130), (1, 400, 400, 8), (1, 2048, 2048, 32),
                                        (2, 700, 1200, 48), (1, 2048, 4096, 32), (1, 1024, 1024, 16),
                                        (1, 2048, 2048, 4), (1, 1500, 1500, 10), (1, 512, 512, 16),
-                                       (1, 4096, 4096, 4), (1, 1500, 1500, 20)])
+                                       (1, 4096, 4096, 4), (1, 1500, 1500, 20), (1, 4096, 4096, 8)])
 def test_causal_block_schedules(cuda, d, b, sq, sk, h, dtype):
     """The causal block schedules, each checked on a few heads: query-block pairs
     (qb, nqb-1-qb) in one block when unpaired blocks would leave the chip
@@ -250,7 +250,7 @@ def test_causal_block_schedules(cuda, d, b, sq, sk, h, dtype):
     bf16 query blocks over at least 1024 keys split (32 at L = S = 2048: 8 splits;
     60 at L = S = 1500: 4), over 512 keys they do not; 64 to 127 split over 2048
     keys or more (64 at L = S = 4096: 4 splits), not below (120 at L = S = 1500),
-    causal or not."""
+    causal or not; 128 split in two over 4096 keys or more."""
     g = torch.Generator().manual_seed(40 + h)
     q = torch.randn(b, sq, h, d, generator=g).to(dtype).to(cuda)
     k, v = (torch.randn(b, sk, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))
