@@ -11,6 +11,7 @@ import torch
 
 from cpu_attention import flash_attn_func
 from helpers import assert_close, attention, values
+from route_cases import SEEDS as ROUTE_SEEDS, route_case
 
 pytestmark = pytest.mark.gpu
 DTYPES = [torch.float32, torch.bfloat16]
@@ -56,6 +57,39 @@ def test_fuzz(cuda, seed):
     r = random.Random(seed)
     run(r.randint(1, 3), r.randint(1, 900), r.randint(1, 900), r.choice([1, 4, 12]),
         r.choice([32, 64, 128]), r.choice(DTYPES), r.random() < 0.5, seed, cuda)
+
+
+@pytest.mark.parametrize("seed", range(ROUTE_SEEDS))
+def test_route_sweep(cuda, seed):
+    """Seeded shapes weighted toward the route boundaries (short keys either side of
+    256, few query blocks over long keys, a few query rows; route_cases), in three
+    layouts.  Sampled rows of up to 12 (batch, head) pairs are checked against the
+    float64 oracle over exactly the keys each row sees (bottom-right causal; a row
+    that sees none is 0).  The CPU address check replays the same shapes."""
+    b, sq, sk, h, d, dt, causal, layout = route_case(seed)
+    dtype = torch.bfloat16 if dt == "bf16" else torch.float32
+    print(f"route sweep {seed}: b={b} sq={sq} sk={sk} h={h} d={d} {dt} causal={causal} {layout}", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(seed)
+    if layout == "fused":
+        qkv = torch.randn(b, sq, 3 * h * d, generator=g, device=cuda).to(dtype)
+        q, k, v = (qkv[..., i * h * d:(i + 1) * h * d].view(b, sq, h, d) for i in range(3))
+    elif layout == "bhse":
+        q, k, v = (torch.randn(b, h, n, d, generator=g, device=cuda).to(dtype).transpose(1, 2) for n in (sq, sk, sk))
+    else:
+        q, k, v = (torch.randn(b, n, h, d, generator=g, device=cuda).to(dtype) for n in (sq, sk, sk))
+    out = flash_attn_func(q, k, v, causal=causal)
+    r = random.Random(seed)
+    rows = list(range(sq)) if sq * sk <= 300000 else sorted({0, sq - 1, *(r.randrange(sq) for _ in range(24))})
+    pairs = [(bi, hi) for bi in range(b) for hi in range(h)]
+    if len(pairs) > 12:
+        pairs = r.sample(pairs, 12)
+    for bi, hi in pairs:
+        qv, kv, vv, ov = (values(t[bi:bi + 1, :, hi:hi + 1]) for t in (q, k, v, out))
+        ref = []
+        for i in rows:
+            ke = min(sk, max(0, i + 1 + sk - sq)) if causal else sk
+            ref.append(attention(qv[:, i:i + 1], kv[:, :ke], vv[:, :ke], d ** -0.5)[0, 0, 0] if ke else np.zeros(d))
+        assert_close(torch.from_numpy(ov[0, rows, 0]), np.stack(ref), dtype, paged=False)
 
 
 def test_repeated_calls_follow_changes(cuda):

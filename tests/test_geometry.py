@@ -12,6 +12,7 @@ import shutil
 import subprocess
 
 import pytest
+from route_cases import SEEDS as ROUTE_SEEDS, route_case
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 SRC = os.path.join(HERE, "geom_check.hip")
@@ -96,6 +97,10 @@ def shapes():
             for bf16 in (False, True):
                 for lay in ("bshe", "fused"):
                     out.append(line(e, bf16, False, b, sq, sk, h, lay))
+    # the GPU route sweep's shapes (test_flash_gpu.py::test_route_sweep)
+    for seed in range(ROUTE_SEEDS):
+        b, sq, sk, h, e, dt, causal, lay = route_case(seed)
+        out.append(line(e, dt == "bf16", causal, b, sq, sk, h, lay))
     # BASELINE: cfg1, cfg4 (fused q/k/v) and its cross shape
     out.append(line(64, True, True, 1, 128, 128, 16))
     out.append(line(128, True, True, 4, 4096, 4096, 32, "fused"))
