@@ -312,6 +312,14 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
   auto key_of = [&](int j) { return BY_UNIT ? kUnit * (g * UPG + j % UPG) + j / UPG : g + G * j; };
   auto base_of = [&](int j) { return BY_UNIT ? j % UPG : G * j / kUnit; };
   const char* vbase = reinterpret_cast<const char*>(p.vc) + dl * 16;
+  // fp32: odd loads of a batch go to a second set of sums, added at the end, so a
+  // lane's chain over its up to 64 keys of a long tile is two chains of half the
+  // length.  One chain took a row of 81 keys to 1.11e-6 against the reference's
+  // 1e-6 fp32 decode gate; two take it to 6.9e-7, at no measured cost (eight Q.K
+  // chains instead of four cost up to 18% on 256-key tiles and were not kept).
+  float acc2[BF ? 1 : DPL];
+#pragma unroll
+  for (int i = 0; i < (BF ? 1 : DPL); ++i) acc2[i] = 0.f;
 #pragma unroll
   for (int b0 = 0; b0 < R; b0 += B) {
     if (key_of(b0) >= ntok) break;  // the batch's first key (its smallest) is past the tile
@@ -340,13 +348,18 @@ __device__ __forceinline__ void decode_tile(const DecodeParams& p, int64_t seq, 
           st.acc[6] = fmaf(pj, bf16_lo(v.w), st.acc[6]);
           st.acc[7] = fmaf(pj, bf16_hi(v.w), st.acc[7]);
         } else {
-          st.acc[0] = fmaf(pj, __uint_as_float(v.x), st.acc[0]);
-          st.acc[1] = fmaf(pj, __uint_as_float(v.y), st.acc[1]);
-          st.acc[2] = fmaf(pj, __uint_as_float(v.z), st.acc[2]);
-          st.acc[3] = fmaf(pj, __uint_as_float(v.w), st.acc[3]);
+          float* a = (i & 1) ? acc2 : st.acc;
+          a[0] = fmaf(pj, __uint_as_float(v.x), a[0]);
+          a[1] = fmaf(pj, __uint_as_float(v.y), a[1]);
+          a[2] = fmaf(pj, __uint_as_float(v.z), a[2]);
+          a[3] = fmaf(pj, __uint_as_float(v.w), a[3]);
         }
       }
     }
+  }
+  if constexpr (!BF) {
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) st.acc[i] += acc2[i];
   }
 }
 

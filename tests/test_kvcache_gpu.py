@@ -158,6 +158,20 @@ def test_both_tile_sizes(cuda, dtype, d, tiles):
     assert_close(again, ref, dtype, paged=True)
 
 
+def test_fp32_rows_of_long_tiles(cuda):
+    """fp32 rows on 256-key tiles (1856 rows whose page tables span 192 keys), where a
+    lane sums up to 64 keys of P.V.  As one fma chain, the row of 81 keys (sequence
+    79, head 10) reached 1.11e-6 against the reference's 1e-6 gate; the kernel sums a
+    lane's odd and even keys apart and stays inside it.  These are that call's
+    lengths, page size and staging seed (found by a randomized sweep)."""
+    lens = [14, 93, 28, 25, 28, 71, 49, 39, 39, 47, 37, 23, 23, 91, 32, 31, 31, 61, 36, 57, 22, 49, 16, 12,
+            73, 77, 100, 10, 27, 76, 16, 88, 8, 33, 84, 46, 41, 100, 68, 64, 55, 9, 47, 44, 50, 83, 49, 63, 38,
+            93, 42, 82, 30, 14, 1, 46, 37, 37, 1, 57, 76, 97, 88, 26, 38, 6, 56, 56, 16, 0, 35, 25, 75, 92, 10,
+            27, 17, 93, 90, 81, 60, 2, 98, 31, 23, 30, 19, 26, 98, 58, 9, 84, 56, 20, 93, 48, 23, 41, 41, 8,
+            70, 29, 35, 38, 34, 36, 92, 72, 31, 42, 58, 73, 55, 50, 25, 52]
+    decode(lens, 16, 64, 48, torch.float32, seed=137, device=cuda)
+
+
 @pytest.mark.parametrize("host_checks", [True, False])
 def test_uneven_lengths(cuda, host_checks):
     """Lopsided batches (the reference sweeps thread counts here; the GPU splits every
