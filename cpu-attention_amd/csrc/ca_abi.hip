@@ -71,13 +71,16 @@ extern "C" int ca_store(const ca_store_args* a, void* stream) {
 
 // Workspace layout: fp32 partial accumulators [slots, E], then (max, sum) pairs
 // [slots, 2], one slot per (row, block of 8 tiles of the page table's capacity);
-// for calls of at most kMergeMaxRows rows, then one 8-byte counter per row (the
-// in-kernel merge).
+// for calls of kMergeMinRows to kMergeMaxRows rows of at most kMergeMaxBlocks
+// blocks, then one 8-byte counter per row (the in-kernel merge).
 static int64_t decode_acc_bytes(int64_t slots, int64_t head_dim) {
   return ((slots * head_dim * 4 + 255) / 256) * 256;
 }
 
-static bool decode_merges(int64_t rows, int64_t slots) { return slots > 0 && rows <= kMergeMaxRows; }
+// slots = rows x blocks per row (0: every row fits one block).
+static bool decode_merges(int64_t rows, int64_t slots) {
+  return slots > 0 && rows >= kMergeMinRows && rows <= kMergeMaxRows && slots <= rows * kMergeMaxBlocks;
+}
 
 static int64_t decode_ws_bytes(int64_t rows, int64_t head_dim, int64_t page, int64_t width, int tile_keys) {
   const int64_t slots = decode_workspace_slots(rows, decode_tiles(width, page, tile_keys));

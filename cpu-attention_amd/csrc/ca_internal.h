@@ -207,8 +207,21 @@ constexpr int64_t kFusedAppendMaxRows = 1024;
 // 64 rows 11.20 -> 10.38 us, 128 rows 17.89 -> 16.69 us (fp32 H=16 E=64 with an
 // append: 18.24 -> 16.96 us), 512 rows 38.0 -> 37.4 us; 1024 rows even (86.2 ->
 // 85.8 us; fp32 E=64 84.7 -> 85.6 us), 4096 rows (bf16 E=128 page 32) 189.3 ->
-// 191.4 us.
+// 191.4 us.  It also needs at least kMergeMinRows rows and at most kMergeMaxBlocks
+// blocks per row (of the page table's capacity): a row's blocks count themselves
+// in on one counter with a compare-and-swap, and when many finish at once the
+// retries serialise.  Against the combine kernel (bf16 E=128 page 16 unless
+// noted, back-to-back, with a one-token append): N=1 H=8 at 32768 keys (64 blocks
+// per row) 213.1 -> 31.7 us, N=1 H=32 at 32768 keys 157.7 -> 90.6 us, at 4096 (8
+// blocks) 20.5 -> 15.5 us, at 3072 (6) 16.2 -> 13.6 us, at 2560 (5) 14.6 -> 12.6 us,
+// at 2048 (4 blocks, 32 rows of one length) 12.8 -> 11.8 us, fp32 N=2 H=4 E=64 at
+// 20000 keys 94.9 -> 23.2 us; the merge still wins at 4 blocks from 64 rows (fp32
+// N=8 H=16 E=64 at 2048 keys 25.3 -> 24.7 us, cfg2 18.1 -> 17.3 us, N=16 H=32
+// lengths up to 2047 without append 37.4 -> 36.7 us) and is even at 5 blocks
+// over 64 rows (fp32 N=8 H=8 E=64 at 2560 keys 20.5 -> 20.4 us).
 constexpr int64_t kMergeMaxRows = 512;
+constexpr int64_t kMergeMinRows = 64;
+constexpr int64_t kMergeMaxBlocks = 4;
 
 int store_launch(const StoreParams& p, int words, hipStream_t stream);
 // One token per sequence (p.per_seq == 1): one wave per (token, head), no staging.

@@ -85,7 +85,8 @@ def test_flash_declines_a_misaligned_workspace(cuda, dtype, sq):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_decode_merge_counters_in_any_workspace(cuda, dtype):
-    """Calls of at most 512 rows merge their split rows inside the decode kernel:
+    """Calls of 64 to 512 rows of at most 4 blocks merge their split rows inside the
+    decode kernel:
     each block counts itself in on a per-row counter in the workspace, tagged with
     the call, and the row's last block merges.  Whatever the workspace holds
     beforehand (zeros, all-ones bytes, random bytes, small integers, the previous
@@ -93,8 +94,8 @@ def test_decode_merge_counters_in_any_workspace(cuda, dtype):
     gates; a second call shape on the same workspace (its slots and counters
     elsewhere) does too."""
     lib = K.module().lib
-    h, d, page = 8, 128, 16
-    lens = [3000, 17, 1500, 513, 2100, 64]
+    h, d, page = 16, 128, 16
+    lens = [2000, 17, 1500, 513, 1900, 64]  # 96 rows, 2016 keys of page table (4 blocks)
     print(f"decode merge counters dtype={dtype}", flush=True)
     q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=31, device=cuda)
     seqlens = torch.tensor(lens, dtype=torch.int32, device=cuda)
@@ -117,7 +118,7 @@ def test_decode_merge_counters_in_any_workspace(cuda, dtype):
     assert_close(outs[0], reference(q, ks, vs, d ** -0.5), dtype, paged=True)
     for o in outs[1:]:
         assert torch.equal(o.view(torch.uint8), outs[0].view(torch.uint8))
-    lens2 = [2500, 700, 1100]
+    lens2 = [1800, 700, 1100, 90]  # 64 rows, 4 blocks
     q2, kc2, vc2, bt2, ks2, vs2 = stage(lens2, h, d, page, dtype, seed=32, device=cuda)
     assert lib.ca_decode_workspace_bytes(len(lens2), h, d, page, bt2.shape[1]) <= need
     out2 = torch.full_like(q2, float("nan"))
@@ -135,10 +136,36 @@ def test_decode_merge_row_limit(cuda, nseq):
     lib = K.module().lib
     h, d, page, dtype = 32, 64, 16, torch.bfloat16
     rng = np.random.default_rng(nseq)
-    lens = rng.integers(17, 2048, size=nseq).tolist()
+    lens = rng.integers(17, 2000, size=nseq).tolist()  # page tables of at most 4 blocks
     print(f"decode merge row limit nseq={nseq}", flush=True)
     q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=nseq, device=cuda)
     ws = torch.empty(lib.ca_decode_workspace_bytes(nseq, h, d, page, bt.shape[1]), dtype=torch.uint8, device=cuda)
+    out = torch.full_like(q, float("nan"))
+    rc = lib.ca_decode(ctypes.byref(args_for(q, kc, vc, torch.tensor(lens, dtype=torch.int32, device=cuda), bt, out,
+                                             ws)), stream())
+    assert rc == K.CA_OK, lib.ca_status_string(rc)
+    torch.cuda.synchronize()
+    assert_close(out, reference(q, ks, vs, d ** -0.5), dtype, paged=True)
+
+
+@pytest.mark.parametrize("nseq,h,longest,merges", [(2, 32, 2000, True), (2, 32, 2100, False), (1, 32, 2000, False),
+                                                    (1, 8, 30000, False)])
+def test_decode_merge_block_limit(cuda, nseq, h, longest, merges):
+    """The in-kernel merge takes calls of 64 to 512 rows whose page table holds at
+    most 4 blocks (2048 keys of 64-key tiles); more blocks or fewer rows go through
+    the combine kernel (many blocks of a row counting in at once serialise).  The
+    workspace size shows the route (one 8-byte counter per row); both routes match
+    the oracle."""
+    lib = K.module().lib
+    d, page, dtype = 64, 16, torch.bfloat16
+    lens = [longest] + [longest // 3] * (nseq - 1)
+    print(f"decode merge block limit nseq={nseq} h={h} longest={longest}", flush=True)
+    q, kc, vc, bt, ks, vs = stage(lens, h, d, page, dtype, seed=41, device=cuda)
+    need = lib.ca_decode_workspace_bytes(nseq, h, d, page, bt.shape[1])
+    rows, blocks = nseq * h, -(-bt.shape[1] * page // 512)
+    acc = (rows * blocks * d * 4 + 255) // 256 * 256 + rows * blocks * 8
+    assert need == acc + (rows * 8 if merges else 0)
+    ws = torch.empty(need, dtype=torch.uint8, device=cuda)
     out = torch.full_like(q, float("nan"))
     rc = lib.ca_decode(ctypes.byref(args_for(q, kc, vc, torch.tensor(lens, dtype=torch.int32, device=cuda), bt, out,
                                              ws)), stream())
