@@ -104,9 +104,16 @@ extern "C" int64_t ca_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads
                                              int64_t head_dim, int64_t page_size,
                                              int64_t page_table_width) {
   if (num_seqs < 0 || num_heads < 0 || page_size <= 0 || page_table_width < 0) return -1;
+  // The tile size depends on the element size, which the query does not name: it
+  // answers for the larger of the bf16 and the fp32 call.
   const int64_t rows = num_seqs * num_heads;
-  return decode_ws_bytes(rows, head_dim, page_size, page_table_width,
-                         decode_tile_keys(rows, page_table_width, page_size, head_dim));
+  int64_t most = 0;
+  for (int esize : {2, 4}) {
+    const int64_t b = decode_ws_bytes(rows, head_dim, page_size, page_table_width,
+                                      decode_tile_keys(rows, page_table_width, page_size, head_dim, esize));
+    most = b > most ? b : most;
+  }
+  return most;
 }
 
 // ca_decode and ca_decode_noalloc.  The split-K scratch is the caller's workspace,
@@ -128,7 +135,7 @@ static int decode_entry(const ca_decode_args* a, void* stream, bool noalloc) {
   const int64_t have = noalloc ? CA_DECODE_NOALLOC_SCRATCH_BYTES
                                : (a->workspace && aligned16(a->workspace) && a->workspace_bytes > 0
                                       ? a->workspace_bytes : 0);
-  int tile_keys = decode_tile_keys(rows, a->page_table_width, a->page_size, a->head_dim);
+  int tile_keys = decode_tile_keys(rows, a->page_table_width, a->page_size, a->head_dim, a->dtype == CA_BF16 ? 2 : 4);
   int64_t need = decode_ws_bytes(rows, a->head_dim, a->page_size, a->page_table_width, tile_keys);
   if (need > have && tile_keys != kDecodeLongTile) {
     const int64_t need_long = decode_ws_bytes(rows, a->head_dim, a->page_size, a->page_table_width, kDecodeLongTile);

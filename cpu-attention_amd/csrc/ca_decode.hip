@@ -580,17 +580,26 @@ __global__ __launch_bounds__(256) void decode_tiles_combine_kernel(DecodeParams 
 // largest batches (N=64 H=32 E=128, lengths 17..2047: 196 -> 185 us; N=64 H=16
 // E=128 fp32: 276 -> 208 us).  They lose where every row fits one 256-key block
 // (2048 keys, so no combine pass), those blocks already give every CU one (256
-// rows or more), and the call is small: there the combine launch the 64-key
-// tiles need costs more than they save
-// (N=8 H=32 E=64, 2048 keys: 18.2 -> 21.9 us; N=8 H=32 E=32: 16.3 -> 19.2 us).
-// The rule depends on shapes only (not on lengths or dtype), so the workspace size
-// does too.
-int decode_tile_keys(int64_t rows, int64_t pt_width, int64_t page, int64_t head_dim) {
+// rows or more), the call is small, and its rows are narrow (E * esize at most 128
+// bytes: a 256-key tile's K and V within 64 KB): there the merge the 64-key tiles
+// need costs more than they save (bf16 N=8 H=32 E=64 P=32, lengths 17..2047: 14.5
+// -> 16.2 us; E=32: 9.3 -> 12.5 us).  Wider rows load too much per wave for one
+// 256-key tile: bf16 E=128 N=8 H=32 at 2048 keys 53.4 -> 44.5 us, N=16 H=32 at 1024
+// keys 53.1 -> 45.2 us, fp32 E=64 N=64 H=8 at 2048 keys 100.9 -> 86.4 us, fp32
+// E=128 N=16 H=16 at lengths up to 1500 85.2 -> 73.3 us.  A page table of at most
+// 512 keys takes 64-key tiles whatever the rows: one block of them covers a row, so
+// nothing is merged, and a row gets 8 waves instead of 2 (fp32 N=128 H=8 E=128 at 512
+// keys 180.2 -> 103.2 us, bf16 55.5 -> 46.4 us; bf16 N=64 H=32 E=64 59.9 -> 48.7 us;
+// bf16 N=256 H=8 E=64 at 128 keys 22.2 -> 18.6 us).  The rule depends on shapes and
+// the element size only (not on lengths), so the workspace size does too.
+int decode_tile_keys(int64_t rows, int64_t pt_width, int64_t page, int64_t head_dim, int esize) {
   const int64_t cap = pt_width * page;
+  if (cap <= (int64_t)kDecWaves * kShortTile) return kShortTile;
   const bool one_block = cap <= (int64_t)kDecWaves * kTile;
   const bool fills = rows >= 256;
   const bool small = rows * cap * head_dim <= (80ll << 20);  // K elements at capacity
-  return one_block && fills && small ? kTile : kShortTile;
+  const bool narrow = head_dim * esize <= 128;
+  return one_block && fills && small && narrow ? kTile : kShortTile;
 }
 
 int64_t decode_tiles(int64_t pt_width, int64_t page, int tile_keys) { return cdiv(pt_width * page, tile_keys); }

@@ -227,7 +227,7 @@ int store_launch(const StoreParams& p, int words, hipStream_t stream);
 // One token per sequence (p.per_seq == 1): one wave per (token, head), no staging.
 int store_scatter_launch(const StoreParams& p, int words, hipStream_t stream);
 constexpr int kDecodeLongTile = 256;  // keys per tile of the decode's long tiles
-int decode_tile_keys(int64_t rows, int64_t pt_width, int64_t page, int64_t head_dim);
+int decode_tile_keys(int64_t rows, int64_t pt_width, int64_t page, int64_t head_dim, int esize);
 int64_t decode_tiles(int64_t pt_width, int64_t page, int tile_keys);
 int64_t decode_workspace_slots(int64_t rows, int64_t tiles);
 int decode_launch(const DecodeParams& p, int head_dim, int bf16, hipStream_t stream);

@@ -129,12 +129,15 @@ typedef struct ca_decode_args {
 } ca_decode_args;
 
 /* ca_decode_workspace_bytes: the split-K scratch a call of these shapes needs
- * with its preferred tile size (0: none; rows whose page table holds at most one
- * block of tiles, 512 keys with 64-key tiles or 2048 with 256-key tiles, need
- * none): the rows' block partials, and for calls of 64 to 512 rows whose page
+ * with its preferred tile size, for the larger of a bf16 and an fp32 call (the
+ * tile size depends on the element size too: 256-key tiles only for rows of at
+ * most 128 bytes).  0: none; rows whose page table holds at most one block of
+ * tiles, 512 keys with 64-key tiles or 2048 with 256-key tiles, need none.
+ * Otherwise the rows' block partials, and for calls of 64 to 512 rows whose page
  * table holds at most 4 blocks of tiles (whose partials the row's last block
- * merges inside the decode kernel) one 8-byte counter per row, tagged per call, so that no clearing is needed; calls that
- * overlap must not share a workspace.  It is not monotonic in num_seqs: the preferred tile size depends on the
+ * merges inside the decode kernel) one 8-byte counter per row, tagged per call,
+ * so that no clearing is needed; calls that overlap must not share a workspace.
+ * It is not monotonic in num_seqs: the preferred tile size depends on the
  * number of rows.  ca_decode therefore takes 256-key tiles when the workspace it
  * is given is too small for the preferred ones but holds those; with one tile
  * size the need grows with the rows, so a workspace sized once for the largest

@@ -108,32 +108,37 @@ def test_entries_decline_malformed_calls_without_a_gpu():
     f.seq_q = 4
     assert lib.ca_flash(ctypes.byref(f), None) == K.CA_DECLINED  # null pointers
     # decode: one (max, sum, P.V) partial per (row, block of 8 tiles), none when a row
-    # fits one block.  Tiles are 64 keys (512 per block) unless every row fits one
-    # block of 256-key tiles (2048 keys), there are 256 rows or more, and K holds at
-    # most 80 Mi elements at the page table's capacity.
+    # fits one block.  Tiles are 64 keys (512 per block) unless the page table holds
+    # more than 512 keys and every row fits one block of 256-key tiles (2048 keys),
+    # there are 256 rows or more, K holds at most 80 Mi elements at the page table's
+    # capacity, and a row is narrow (E * esize at most 128 bytes).  The query answers
+    # for the larger of the bf16 and the fp32 call.
     def partials(rows, blocks, d, merges=None):
         # accumulators (256-byte aligned), (max, sum) pairs, and for calls of 64 to
         # 512 rows of at most 4 blocks one 8-byte merge counter per row
         if merges is None:
             merges = 64 <= rows <= 512 and blocks <= 4
         return ((rows * blocks * d * 4 + 255) // 256) * 256 + rows * blocks * 2 * 4 + (rows * 8 if merges else 0)
-    assert lib.ca_decode_workspace_bytes(8, 32, 64, 32, 64) == 0          # 256-key tiles
+    assert lib.ca_decode_workspace_bytes(8, 32, 32, 32, 64) == 0          # 256-key tiles in either dtype
+    assert lib.ca_decode_workspace_bytes(8, 32, 64, 32, 64) == partials(256, 4, 64)  # fp32 E=64: 64-key tiles
     assert lib.ca_decode_workspace_bytes(64, 32, 128, 32, 64) == partials(2048, 4, 128)
-    assert lib.ca_decode_workspace_bytes(4, 32, 64, 32, 64) == partials(128, 4, 64)  # < 256 rows
-    assert lib.ca_decode_workspace_bytes(8, 32, 64, 32, 65) == partials(256, 5, 64)  # > 2048 keys
+    assert lib.ca_decode_workspace_bytes(4, 32, 32, 32, 64) == partials(128, 4, 32)  # < 256 rows
+    assert lib.ca_decode_workspace_bytes(8, 32, 32, 32, 65) == partials(256, 5, 32)  # > 2048 keys
     assert lib.ca_decode_workspace_bytes(1, 32, 128, 16, 32) == 0          # 512 keys: one block
+    assert lib.ca_decode_workspace_bytes(128, 8, 32, 16, 32) == 0          # 512 keys, 1024 rows: one block
+    assert lib.ca_decode_workspace_bytes(8, 32, 128, 16, 128) == partials(256, 4, 128)  # wide rows
     # the in-kernel merge's counters: 64 to 512 rows of at most 4 blocks
     assert lib.ca_decode_workspace_bytes(2, 32, 64, 16, 128) == partials(64, 4, 64)
     assert partials(64, 4, 64) == partials(64, 4, 64, merges=False) + 64 * 8
     assert lib.ca_decode_workspace_bytes(1, 32, 64, 16, 128) == partials(32, 4, 64, merges=False)  # 32 rows
     assert lib.ca_decode_workspace_bytes(2, 32, 64, 16, 129) == partials(64, 5, 64, merges=False)  # 5 blocks
     assert lib.ca_decode_workspace_bytes(1, 8, 128, 16, 2048) == partials(8, 64, 128, merges=False)
-    # not monotonic in the batch: 8 sequences of H=32 over 2048 keys prefer 256-key
-    # tiles (no partials), 7 prefer 64-key tiles (ca_decode then takes 256-key tiles
-    # when its workspace holds only theirs), 11 exceed 80 Mi K elements
-    assert lib.ca_decode_workspace_bytes(8, 32, 128, 16, 128) == 0
-    assert lib.ca_decode_workspace_bytes(7, 32, 128, 16, 128) == partials(224, 4, 128)
-    assert lib.ca_decode_workspace_bytes(11, 32, 128, 16, 128) == partials(352, 4, 128)
+    # not monotonic in the batch: 8 sequences of H=32 E=32 over 2048 keys prefer
+    # 256-key tiles (no partials), 7 prefer 64-key tiles (ca_decode then takes 256-key
+    # tiles when its workspace holds only theirs), 41 exceed 80 Mi K elements
+    assert lib.ca_decode_workspace_bytes(8, 32, 32, 16, 128) == 0
+    assert lib.ca_decode_workspace_bytes(7, 32, 32, 16, 128) == partials(224, 4, 32)
+    assert lib.ca_decode_workspace_bytes(41, 32, 32, 16, 128) == partials(1312, 4, 32)
     assert lib.ca_flash_workspace_bytes(1, 1, 1, 1, 64, 1) == 0
 
 

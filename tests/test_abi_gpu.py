@@ -20,15 +20,15 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_decode_workspace_sized_for_the_largest_batch(cuda, dtype):
-    """H=32, E=128, 16-token pages, a page table of 2048 keys: 8 sequences (256
+    """H=32, E=32, 16-token pages, a page table of 2048 keys: 8 sequences (256
     rows) prefer 256-key tiles and need no workspace; 7 sequences prefer 64-key
     tiles, whose partials need some.  Sized for the 8, the 7 run on 256-key tiles;
-    11 sequences need a workspace again, and one sized for them serves 7 too."""
+    41 sequences need a workspace again, and one sized for them serves 7 too."""
     lib = K.module().lib
-    h, d, page, width = 32, 128, 16, 128
+    h, d, page, width = 32, 32, 16, 128
     assert lib.ca_decode_workspace_bytes(8, h, d, page, width) == 0
     assert lib.ca_decode_workspace_bytes(7, h, d, page, width) > 0
-    need11 = lib.ca_decode_workspace_bytes(11, h, d, page, width)
+    need11 = lib.ca_decode_workspace_bytes(41, h, d, page, width)
     assert need11 > lib.ca_decode_workspace_bytes(7, h, d, page, width)
     lens = [2030, 17, 1500, 512, 513, 2000, 64]
     print(f"decode workspace sizing dtype={dtype}", flush=True)

@@ -122,31 +122,33 @@ def test_scatter_store_of_one_token_per_sequence(cuda, dtype, d, h, mode):
     np.testing.assert_array_equal(cache_words(vc), vw)
 
 
-def long_tile_waves(nseqs, h, width, page):
-    """256-key tiles the decode's rows hold at the page table's capacity; the kernel
-    takes 64-key tiles when this is at most 2048 (csrc/ca_decode.hip)."""
-    return nseqs * h * -(-width * page // 256)
+def long_tiles(rows, width, page, d, esize):
+    """Whether the decode takes 256-key tiles (csrc/ca_decode.hip, decode_tile_keys):
+    a page table of more than 512 keys and at most 2048, 256 rows or more, at most
+    80 Mi K elements at capacity, rows of at most 128 bytes."""
+    cap = width * page
+    return 512 < cap <= 2048 and rows >= 256 and rows * cap * d <= 80 << 20 and d * esize <= 128
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("d", [32, 64, 128])
-@pytest.mark.parametrize("tiles", ["short", "long"])
+@pytest.mark.parametrize("dtype,d,tiles", [(dt, d, "short") for dt in DTYPES for d in (32, 64, 128)] +
+                         [(torch.bfloat16, 32, "long"), (torch.bfloat16, 64, "long"), (torch.float32, 32, "long")])
 def test_both_tile_sizes(cuda, dtype, d, tiles):
     """A batch on each side of the 64/256-key tile choice, with rows at the edges of
     tiles and of blocks (512 keys of 64-key tiles, 2048 of 256-key tiles) and rows
-    that span several blocks and meet in the combine kernel: a one-token append
-    attended in the same call, then a plain decode of the same cache."""
+    that span several blocks and are merged: a one-token append attended in the same
+    call, then a plain decode of the same cache.  256-key tiles serve only narrow
+    rows (bf16 E <= 64, fp32 E = 32)."""
     page = 16
     if tiles == "short":
         h, lens = 2, [0, 63, 64, 511, 512, 513, 1100, 3000]
     else:
         h, rng = 8, random.Random(d)
-        lens = [0, 255, 256, 2047, 2048, 2049, 2100] + [rng.randrange(0, 2101) for _ in range(57)]
+        lens = [0, 255, 256, 1023, 1024, 2029, 2030] + [rng.randrange(0, 2031) for _ in range(57)]
     # staged with one token more than lens, so that position lens[s] lies in a page of
     # sequence s; the append overwrites that token
     q, kc, vc, bt, ks, vs = stage([n + 1 for n in lens], h, d, page, dtype, seed=d, device=cuda)
-    waves = long_tile_waves(len(lens), h, bt.shape[1], page)
-    assert (waves <= 2048) == (tiles == "short")
+    esize = 2 if dtype == torch.bfloat16 else 4
+    assert long_tiles(len(lens) * h, bt.shape[1], page, d, esize) == (tiles == "long")
     ks, vs = [k[:, :n] for k, n in zip(ks, lens)], [v[:, :n] for v, n in zip(vs, lens)]
     g = torch.Generator().manual_seed(d)
     kn, vn = (torch.randn(len(lens), 1, h, d, generator=g).to(dtype).to(cuda) for _ in range(2))
@@ -159,11 +161,12 @@ def test_both_tile_sizes(cuda, dtype, d, tiles):
 
 
 def test_fp32_rows_of_long_tiles(cuda):
-    """fp32 rows on 256-key tiles (1856 rows whose page tables span 192 keys), where a
-    lane sums up to 64 keys of P.V.  As one fma chain, the row of 81 keys (sequence
-    79, head 10) reached 1.11e-6 against the reference's 1e-6 gate; the kernel sums a
-    lane's odd and even keys apart and stays inside it.  These are that call's
-    lengths, page size and staging seed (found by a randomized sweep)."""
+    """fp32 rows of 1856 rows whose page tables span 192 keys.  On 256-key tiles, as
+    this call then ran, a lane summed up to 64 keys of P.V in one fma chain, and the
+    row of 81 keys (sequence 79, head 10) reached 1.11e-6 against the reference's
+    1e-6 gate; the kernel now sums a lane's odd and even keys apart, and page tables
+    of at most 512 keys take 64-key tiles.  These are that call's lengths, page size
+    and staging seed (found by a randomized sweep)."""
     lens = [14, 93, 28, 25, 28, 71, 49, 39, 39, 47, 37, 23, 23, 91, 32, 31, 31, 61, 36, 57, 22, 49, 16, 12,
             73, 77, 100, 10, 27, 76, 16, 88, 8, 33, 84, 46, 41, 100, 68, 64, 55, 9, 47, 44, 50, 83, 49, 63, 38,
             93, 42, 82, 30, 14, 1, 46, 37, 37, 1, 57, 76, 97, 88, 26, 38, 6, 56, 56, 16, 0, 35, 25, 75, 92, 10,
