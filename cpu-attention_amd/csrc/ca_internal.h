@@ -140,13 +140,17 @@ constexpr int64_t kRowsMaxSplits = 64;
 // splits 152.0 us.  bf16 calls with fewer than twice as many keys as rows do not split
 // from 2 * kTiledMinItemsUnsplit query blocks under 2 * kTiledMinKeysLong keys (more
 // query blocks than that round down to one split anyway), nor from
-// kTiledMinItemsUnsplit under kTiledMinKeysLong keys, nor, if causal, under
-// kTiledMinKeysCausal keys: the
+// kTiledMinItemsUnsplit under kTiledMinKeysLong keys, nor, if causal or from
+// kTiledMinItemsShort query blocks, under kTiledMinKeysCausal keys: the
 // partials (fp32 (E + 2) per row and split, written and read back) and, for causal
 // calls, a triangle that is most of the work make the unsplit blocks finish sooner
 // (N=1 L=S=1024 H=32 E=128 non-causal 39.7 -> 31.3 us, causal 41.1 -> 33.8 us;
 // L=S=1500 H=20 E=64: 34.6 -> 31.5 us; causal L=S=512 H=16 E=64, 32 query blocks,
-// 18.6 -> 16.6 us).  With fewer query blocks, or 64 to 127 over longer keys, most
+// 18.6 -> 16.6 us; non-causal N=2 L=S=600 H=8 E=64, 48 blocks, 20.5 -> 17.3 us;
+// N=1 L=S=512 H=8 E=128, 16 blocks, 20.7 -> 20.0 us).  Non-causal calls of fewer
+// blocks under 1024 keys still split (N=1 L=S=768 H=4 E=128, 12 blocks: 20.8 split
+// against 25.3 us; N=1 L=S=1000 H=2 E=64, 8: 15.5 against 23.2 us).  With fewer
+// query blocks, or 64 to 127 over longer keys, most
 // CUs would sit idle unsplit (N=2 L=700 S=1200 H=8 E=64, 48 blocks: split 23.0 us,
 // unsplit 26.1 us; N=1 L=S=4096 H=4 E=128, 64: non-causal 51.6 against 96.1 us,
 // causal 47.0 against 97.2 us; L=S=2048 H=8 E=64 26.3 / 27.9 against 38.6 / 40.8
@@ -160,6 +164,7 @@ constexpr int64_t kTiledMinKeys = 256;
 constexpr int64_t kTiledMaxSplits = 64;
 constexpr int64_t kTiledMinItemsUnsplit = 64;
 constexpr int64_t kTiledMinKeysCausal = 1024;
+constexpr int64_t kTiledMinItemsShort = 16;
 constexpr int64_t kTiledMinKeysLong = 2048;
 __host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, int64_t seq_k, int64_t heads,
                                                 bool bf16, bool causal) {
@@ -169,7 +174,7 @@ __host__ __device__ inline int64_t tiled_splits(int64_t batch, int64_t seq_q, in
   if (bf16 && seq_k < 2 * seq_q &&
       ((items >= 2 * kTiledMinItemsUnsplit && seq_k < 2 * kTiledMinKeysLong) ||
        (items >= kTiledMinItemsUnsplit && seq_k < kTiledMinKeysLong) ||
-       (causal && seq_k < kTiledMinKeysCausal)))
+       (seq_k < kTiledMinKeysCausal && (causal || items >= kTiledMinItemsShort))))
     return 1;
   const int64_t target = bf16 ? kTiledTargetBlocks : 2 * kTiledTargetBlocks;
   if (items <= 0 || items >= target) return 1;

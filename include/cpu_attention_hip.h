@@ -187,7 +187,7 @@ int ca_decode_noalloc(const ca_decode_args* args, void* stream);
  * than 256 query blocks of 256 rows (bf16) or 512 of 128 rows (fp32) over long
  * key ranges (bf16 calls with fewer than twice as many keys as rows only below
  * 64 query blocks, below 128 over 2048 keys or more, or at 128 over 4096 or
- * more; causal ones only over 1024 keys or more).
+ * more; under 1024 keys only non-causal calls below 16 query blocks).
  * Pass at least the bytes ca_flash_workspace_bytes() asks for (0 means none is
  * needed; it answers for the larger of the causal and non-causal call; a
  * shorter workspace declines the call), 16-byte aligned (256 recommended; a

@@ -194,7 +194,7 @@ def tiled(b, sq, sk, h, d, dtype):
     each (whole 64-key units) and at most 64 splits, which needs (E + 2) floats
     per (batch, head, row, split).  bf16 calls with fewer than twice as many keys
     as rows do not split from 128 query blocks under 4096 keys, nor from 64 under
-    2048 keys, nor, if causal, under 1024 keys.  The query answers for the larger
+    2048 keys, nor, if causal or from 16 query blocks, under 1024 keys.  The query answers for the larger
     of the causal and non-causal call."""
     blocks = b * h * -(-sq // (256 if dtype == 1 else 128))
     target = 256 if dtype == 1 else 512
@@ -203,7 +203,7 @@ def tiled(b, sq, sk, h, d, dtype):
         if blocks >= target:
             return 1
         if dtype == 1 and sk < 2 * sq and ((blocks >= 128 and sk < 4096) or (blocks >= 64 and sk < 2048) or
-                                           (causal and sk < 1024)):
+                                           (sk < 1024 and (causal or blocks >= 16))):
             return 1
         per = target // blocks if dtype == 1 else -(-target // blocks)
         return min(per, -(-sk // 64) // 4, 64)
@@ -244,6 +244,9 @@ def test_flash_workspace_for_split_keys(d):
     # 128 query blocks over 4096 keys: 2 splits (more than 128 round down to 1)
     assert lib.ca_flash_workspace_bytes(1, 4096, 4096, 8, d, 1) == 8 * 4096 * 2 * (d + 2) * 4
     assert lib.ca_flash_workspace_bytes(1, 4096, 4096, 12, d, 1) == 0
+    # under 1024 keys: no split from 16 query blocks, causal or not
+    assert lib.ca_flash_workspace_bytes(2, 600, 600, 8, d, 1) == 0
+    assert lib.ca_flash_workspace_bytes(1, 768, 768, 4, d, 1) > 0  # 12 blocks split
 
 
 def test_missing_library_is_a_loud_error(monkeypatch):

@@ -330,6 +330,16 @@ def test_split_keys(cuda, d, causal, shape, dtype):
     run(b, sq, sk, h, d, dtype, causal, 31 + sq, cuda)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("b,sq,sk,h", [(2, 600, 600, 8), (1, 512, 512, 8), (1, 768, 768, 4), (1, 1000, 1000, 2)])
+def test_short_key_split_rule(cuda, d, b, sq, sk, h):
+    """bf16 non-causal calls under 1024 keys (fewer than twice as many keys as
+    rows): from 16 query blocks unsplit (48 and 16 here), below it their keys split
+    over blocks (12 and 8)."""
+    print(f"short-key split rule b={b} sq={sq} sk={sk} h={h} d={d}", flush=True)
+    run(b, sq, sk, h, d, torch.bfloat16, False, 61 + sq, cuda)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_split_keys_rows_without_keys(cuda, dtype):
     """Causal with more query rows than keys: the first rows see no key (exactly

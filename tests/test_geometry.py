@@ -87,7 +87,8 @@ def shapes():
     # calls with keys under twice the rows that split (few query blocks)
     for e in (64, 128):
         for b, sq, sk, h in [(1, 4096, 4096, 4), (1, 2048, 2048, 12), (1, 1024, 1024, 8), (1, 3000, 3000, 8),
-                             (1, 1500, 2100, 16), (1, 4096, 4096, 8), (1, 8192, 8192, 4)]:
+                             (1, 1500, 2100, 16), (1, 4096, 4096, 8), (1, 8192, 8192, 4), (2, 600, 600, 8),
+                             (1, 768, 768, 4), (1, 512, 512, 8), (1, 1000, 1000, 2)]:
             for causal in (False, True):
                 out.append(line(e, True, causal, b, sq, sk, h, "fused"))
     # single-row calls on the packed-heads route (split keys, merge counters)
