@@ -81,6 +81,14 @@ struct FlashParams {
 constexpr int64_t kRowsMaxL = 16;
 constexpr int64_t kRowsMaxLFew = 8;
 constexpr int kRowsPerWave = 4;
+// fp32 calls of 13 to 16 rows: kRowsPerWaveMany rows per wave, so two waves
+// instead of four read each key (bit-identical results).  Measured on MI355X,
+// back-to-back: N=16 L=16 S=4096 H=32 E=128 1212 -> 968 us, E=64 causal 568 -> 450
+// us, N=2 L=16 S=8192 H=128 E=64 551 -> 434 us, N=8 L=16 S=1024 H=32 E=128 167 -> 134
+// us; at 12 rows (3 waves against 2) it lost (N=4 L=12 S=3000 H=64 E=128 340 -> 366
+// us), at 9 it was even.
+constexpr int kRowsPerWaveMany = 8;
+constexpr int64_t kRowsManyMinL = 13;
 __host__ __device__ inline bool rows_route(int64_t batch, int64_t seq_q, int64_t heads, bool bf16) {
   if (bf16) return seq_q <= 4;
   return seq_q <= kRowsMaxLFew || (seq_q <= kRowsMaxL && batch * heads >= 256);
@@ -246,7 +254,7 @@ int decode_noalloc_ordered(int device, hipStream_t stream, const std::function<i
 enum { kPlanDeclined = 0, kPlanNone, kPlanRows, kPlanRowsHeads, kPlanBf16, kPlanF32, kPlanSmall };
 struct FlashPlan {
   int kind;
-  int rows_r;      // kPlanRows: query rows per wave group (1 or kRowsPerWave)
+  int rows_r;      // kPlanRows: query rows per wave group (1, kRowsPerWave or kRowsPerWaveMany)
   bool split;      // kPlanBf16 / kPlanF32: keys split over gy blocks
   bool pair;       // kPlanF32: causal query-block pairs
   int64_t gx, gy;  // grid

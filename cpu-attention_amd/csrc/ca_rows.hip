@@ -48,8 +48,11 @@ __host__ __device__ inline int64_t rows_chunk_keys(int E, bool bf16) {
 }
 
 // Query rows per wave: one for single-row calls (the deepest load ring fits),
-// else kRowsPerWave.
-__host__ __device__ inline int rows_per_wave(int64_t seq_q) { return seq_q == 1 ? 1 : kRowsPerWave; }
+// kRowsPerWaveMany from kRowsManyMinL rows (fp32 only: bf16 calls of more than 4
+// rows take the tiled kernel), else kRowsPerWave.
+__host__ __device__ inline int rows_per_wave(int64_t seq_q) {
+  return seq_q == 1 ? 1 : (seq_q >= kRowsManyMinL ? kRowsPerWaveMany : kRowsPerWave);
+}
 
 // Keys row i may see: [0, kend).
 __host__ __device__ inline int64_t rows_kend(const FlashParams& p, int64_t i) {
@@ -290,6 +293,9 @@ template <int E, bool BF, int R_>
 __global__ __launch_bounds__(64 * kRowsWaves) void flash_rows_kernel(FlashParams p) {
   using S = RowsShape<E, BF, R_>;
   constexpr int DPL = S::DPL, G = S::G, CH = S::CH, R = S::R, W = kRowsWaves, NSTEP = S::NSTEP, NBUF = S::NBUF;
+  // The row counts the routes use and the tests cover (16 rows per wave gave wrong
+  // results when tried, so the kernel admits only these).
+  static_assert(R == 1 || R == kRowsPerWave || R == kRowsPerWaveMany, "rows per wave");
   constexpr int PS = E + 2;  // floats per partial: acc[E], m, l
   __shared__ float part[W][R][PS];
   const int lane = threadIdx.x & 63;
@@ -651,6 +657,9 @@ static int rows_launch_t(const FlashParams& p, const FlashPlan& plan, hipStream_
   else if (R == 1)
     hipLaunchKernelGGL((flash_rows_kernel<E, BF, 1>), dim3((unsigned)gx, (unsigned)splits), dim3(64 * kRowsWaves),
                        0, stream, p);
+  else if (R == kRowsPerWaveMany)
+    hipLaunchKernelGGL((flash_rows_kernel<E, BF, kRowsPerWaveMany>), dim3((unsigned)gx, (unsigned)splits),
+                       dim3(64 * kRowsWaves), 0, stream, p);
   else
     hipLaunchKernelGGL((flash_rows_kernel<E, BF, kRowsPerWave>), dim3((unsigned)gx, (unsigned)splits),
                        dim3(64 * kRowsWaves), 0, stream, p);

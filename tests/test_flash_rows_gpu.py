@@ -40,14 +40,25 @@ def test_few_rows_shapes(cuda, dtype, d, sq, sk, causal):
 
 @pytest.mark.parametrize("dtype,sq,h", [(torch.bfloat16, 4, 4), (torch.bfloat16, 5, 4),
                                         (torch.float32, 8, 4), (torch.float32, 9, 4),
-                                        (torch.float32, 13, 128), (torch.float32, 16, 128),
+                                        (torch.float32, 12, 128), (torch.float32, 13, 128), (torch.float32, 16, 128),
                                         (torch.float32, 17, 128)])
 def test_route_boundary(cuda, dtype, sq, h):
     """The last row count of the few-rows route and the first of the tiled one
     both agree with the oracle: bf16 4 | 5; fp32 8 | 9 with 8 (batch, head) pairs,
-    and 16 | 17 with 256 pairs (13 and 16 rows: row groups of 4, the last one
-    partial or full)."""
+    and 16 | 17 with 256 pairs (12 rows: three row groups of 4; 13 and 16 rows: row
+    groups of 8, the last one partial or full)."""
     run(2, sq, 700, h, 64, dtype, True, seed=sq, device=cuda)
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("sq,sk", [(13, 100), (16, 2000), (14, 4096)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_fp32_row_groups_of_eight(cuda, d, sq, sk, causal):
+    """fp32 calls of 13 to 16 rows with 256 (batch, head) pairs run 8 rows per wave
+    (two waves read each key instead of four): partial and full groups, causal rows
+    that see fewer keys than the group's widest, short and long key ranges."""
+    print(f"fp32 row groups of eight sq={sq} sk={sk} d={d} causal={causal}", flush=True)
+    run(4, sq, sk, 64, d, torch.float32, causal, seed=sq * 100 + d, device=cuda)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

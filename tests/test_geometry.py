@@ -102,6 +102,11 @@ def shapes():
     for seed in range(ROUTE_SEEDS):
         b, sq, sk, h, e, dt, causal, lay = route_case(seed)
         out.append(line(e, dt == "bf16", causal, b, sq, sk, h, lay))
+    # fp32 few-rows calls of 12 to 16 rows over 256 (batch, head) pairs (4 and 8 rows per wave)
+    for b, sq, sk, h in [(4, 13, 100, 64), (4, 16, 2000, 64), (4, 14, 4096, 64), (2, 12, 700, 128), (16, 16, 4096, 32)]:
+        for e in (32, 64, 128):
+            for causal in (False, True):
+                out.append(line(e, False, causal, b, sq, sk, h))
     # BASELINE: cfg1, cfg4 (fused q/k/v) and its cross shape
     out.append(line(64, True, True, 1, 128, 128, 16))
     out.append(line(128, True, True, 4, 4096, 4096, 32, "fused"))
